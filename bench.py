@@ -1,0 +1,290 @@
+"""Benchmark of the north-star workloads on one MI355X.
+
+Prints one JSON line (the driver's contract). The headline workload is BASELINE config 2
+(`configs[1]`): row softmax over fp32 [4096, 8192]; `value` is its whole-job GB/s with
+inputs resident in HBM. The same run measures every other config (vector add 2^28,
+RMSNorm, fp16 4096^3 matmul and + bias + GELU, bf16 flash attention causal 4096 and
+non-causal 1024, int32 histogram and cumsum) and reports them under "workloads", each with
+its roofline fraction. Kernel times come from HIP events recorded on the launch stream
+around the timed launches; inputs rotate over several buffer sets totalling > 512 MB so
+the 256 MB Infinity Cache can't serve them.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME[,NAME]]
+                       [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+os.environ.setdefault("ENCELADUS_CACHE_DIR", os.path.join(ROOT, ".ek_cache"))
+
+HBM_PEAK = 8.0e12          # bytes/s (MI355X HBM3E)
+MFMA_PEAK_F16 = 2.5e15     # dense fp16/bf16 FLOP/s
+GIB = 1 << 30
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Timer:
+    """HIP-event timing on torch's current stream (the stream kernels launch on)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def run(self, launches, steps, warmup):
+        torch = self.torch
+        for i in range(warmup):
+            launches[i % len(launches)]()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for i in range(steps):
+            launches[i % len(launches)]()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / steps  # ms per launch
+
+
+def make_launch(jfn, grid, args, num_warps=4, dot_warps=None, **constexprs):
+    import ctypes
+    from enceladus_amd.runtime import hip
+    vals = jfn._bind(args, constexprs)
+    lc = jfn._lookup(vals, num_warps, dot_warps)
+    packed = []
+    for n in lc.runtime_names:
+        v = vals[n]
+        packed.append(v.data_ptr() if hasattr(v, "data_ptr") else v)
+    kern = lc.ck.pack(packed)
+    buf = ctypes.create_string_buffer(kern, len(kern))
+    fn = lc.ck.function()
+    g = (tuple(grid) + (1, 1, 1))[:3]
+    blk = lc.ck.gen.block
+    lib = hip.load_library()
+    err = ctypes.create_string_buffer(256)
+    import torch
+    stream = ctypes.c_void_p(int(torch.cuda.current_stream().cuda_stream) or None)
+
+    def launch():
+        rc = lib.ek_launch(stream, fn, g[0], g[1], g[2], blk, 1, 1, 0, buf, len(kern), err, 256)
+        if rc:
+            raise RuntimeError(err.value.decode())
+    launch.ck = lc.ck
+    return launch
+
+
+def sets_for(bytes_per_set):
+    return max(2, math.ceil(600e6 / bytes_per_set))
+
+
+# ------------------------------------------------------------------------- workloads
+
+def w_softmax(torch, timer, steps, warmup):
+    from examples.softmax import softmax_kernel
+    M, N = 4096, 8192
+    nbytes = M * N * 4 * 2
+    k = sets_for(nbytes)
+    xs = [torch.randn(M, N, device="cuda", generator=None) for _ in range(k)]
+    outs = [torch.empty_like(x) for x in xs]
+    launches = [make_launch(softmax_kernel, (M,), (o, x, N, N, N), BLOCK=8192)
+                for x, o in zip(xs, outs)]
+    ms = timer.run(launches, steps, warmup)
+    return {"name": "softmax", "config": "fp32 [4096, 8192]", "ms": ms,
+            "bytes": nbytes, "gbps": nbytes / ms / 1e6, "bound": "hbm",
+            "kernel": launches[0].ck.name}
+
+
+def w_rmsnorm(torch, timer, steps, warmup):
+    from examples.rmsnorm import rmsnorm_kernel
+    M, N = 4096, 8192
+    nbytes = M * N * 4 * 2 + N * 4
+    k = sets_for(nbytes)
+    g = torch.Generator(device="cpu").manual_seed(1)
+    w = (torch.rand(N, generator=g) + 0.5).cuda()
+    xs = [torch.randn(M, N, device="cuda") for _ in range(k)]
+    outs = [torch.empty_like(x) for x in xs]
+    launches = [make_launch(rmsnorm_kernel, (M,), (x, w, o, N, N, N, 1e-6), BLOCK=8192)
+                for x, o in zip(xs, outs)]
+    ms = timer.run(launches, steps, warmup)
+    return {"name": "rmsnorm", "config": "fp32 [4096, 8192] eps 1e-6", "ms": ms,
+            "bytes": nbytes, "gbps": nbytes / ms / 1e6, "bound": "hbm",
+            "kernel": launches[0].ck.name}
+
+
+def w_vector_add(torch, timer, steps, warmup):
+    from examples.vector_add import add_kernel
+    n = 1 << 28
+    nbytes = 12 * n
+    xs = [torch.randn(n, device="cuda") for _ in range(2)]
+    y = torch.ones(n, device="cuda")
+    out = torch.empty(n, device="cuda")
+    launches = [make_launch(add_kernel, (n // 1024,), (x, y, out, n), BLOCK=1024) for x in xs]
+    ms = timer.run(launches, max(4, steps // 4), max(2, warmup // 4))
+    return {"name": "vector_add", "config": "fp32 n=2^28 BLOCK 1024", "ms": ms,
+            "bytes": nbytes, "gbps": nbytes / ms / 1e6, "bound": "hbm",
+            "kernel": launches[0].ck.name}
+
+
+def w_matmul(torch, timer, steps, warmup, fused=False):
+    from examples.matmul import matmul_desc_kernel
+    from examples.matmul_fused import matmul_bias_gelu_kernel
+    M = N = K = 4096
+    g = torch.Generator(device="cpu").manual_seed(0)
+    a = (torch.randn(M, K, generator=g) / 64).half().cuda()
+    b = (torch.randn(K, N, generator=g) / 64).half().cuda()
+    bias = torch.randn(N, generator=g).half().cuda()
+    c = torch.empty(M, N, dtype=torch.float16, device="cuda")
+    cfg = dict(BM=128, BN=128, BK=64)
+    grid = (N // 128, M // 128)
+    if fused:
+        l = make_launch(matmul_bias_gelu_kernel, grid, (a, b, bias, c, M, N, K, K, N, N), **cfg)
+    else:
+        l = make_launch(matmul_desc_kernel, grid, (a, b, c, M, N, K, K, N, N), **cfg)
+    ms = timer.run([l], max(5, steps // 2), max(2, warmup // 2))
+    flop = 2 * M * N * K
+    return {"name": "matmul_gelu" if fused else "matmul", "config": "fp16 4096^3 fp32 acc"
+            + (" + bias + GELU" if fused else ""), "ms": ms, "flop": flop,
+            "tflops": flop / ms / 1e9, "bound": "mfma", "kernel": l.ck.name}
+
+
+def w_attention(torch, timer, steps, warmup, causal=True, n=4096):
+    from examples.flash_attention import attention_kernel
+    B, H, D = 4, 32, 128
+    g = torch.Generator(device="cpu").manual_seed(0)
+    q, k, v = (torch.randn(B, H, n, D, generator=g).bfloat16().cuda() for _ in range(3))
+    o = torch.empty_like(q)
+    l = make_launch(attention_kernel, (n // 128, B * H), (q, k, v, o, D ** -0.5, n, n * D, D),
+                    HEAD_DIM=D, BLOCK_M=128, BLOCK_N=64, CAUSAL=causal, dot_warps=(4, 1))
+    ms = timer.run([l], max(3, steps // 4), max(1, warmup // 4))
+    flop = 4 * B * H * n * n * D // (2 if causal else 1)
+    return {"name": f"attention_{'causal' if causal else 'noncausal'}_{n}",
+            "config": f"bf16 [4,32,{n},128] {'causal' if causal else 'non-causal'}", "ms": ms,
+            "flop": flop, "tflops": flop / ms / 1e9, "bound": "mfma", "kernel": l.ck.name}
+
+
+def w_histogram(torch, timer, steps, warmup):
+    from examples.histogram import histogram_kernel
+    n = 1 << 26
+    g = torch.Generator(device="cpu").manual_seed(0)
+    xs = [torch.randint(0, 1024, (n,), generator=g, dtype=torch.int32).cuda() for _ in range(3)]
+    h = torch.zeros(1024, dtype=torch.int32, device="cuda")
+    launches = [make_launch(histogram_kernel, (n // 1024,), (x, h, n, 0.0, 1.0), NUM_BINS=1024,
+                            BLOCK=1024) for x in xs]
+    ms = timer.run(launches, max(4, steps // 4), 2)
+    nbytes = 4 * n
+    return {"name": "histogram", "config": "int32 2^26 -> 1024 bins", "ms": ms, "bytes": nbytes,
+            "gbps": nbytes / ms / 1e6, "bound": "hbm", "kernel": launches[0].ck.name}
+
+
+def w_cumsum(torch, timer, steps, warmup):
+    from examples.cumsum import cumsum_kernel
+    M, N = 8192, 4096
+    nbytes = M * N * 4 * 2
+    g = torch.Generator(device="cpu").manual_seed(0)
+    xs = [torch.randint(-100, 100, (M, N), generator=g, dtype=torch.int32).cuda()
+          for _ in range(sets_for(nbytes))]
+    outs = [torch.empty_like(x) for x in xs]
+    launches = [make_launch(cumsum_kernel, (M,), (o, x, M, N, N, N), REVERSE=False, BLOCK_M=1,
+                            BLOCK_N=4096) for x, o in zip(xs, outs)]
+    ms = timer.run(launches, steps, warmup)
+    return {"name": "cumsum", "config": "int32 [8192, 4096] rows", "ms": ms, "bytes": nbytes,
+            "gbps": nbytes / ms / 1e6, "bound": "hbm", "kernel": launches[0].ck.name}
+
+
+WORKLOADS = {
+    "softmax": w_softmax, "rmsnorm": w_rmsnorm, "vector_add": w_vector_add,
+    "matmul": lambda t, tm, s, w: w_matmul(t, tm, s, w, False),
+    "matmul_gelu": lambda t, tm, s, w: w_matmul(t, tm, s, w, True),
+    "attention_causal": lambda t, tm, s, w: w_attention(t, tm, s, w, True, 4096),
+    "attention_noncausal": lambda t, tm, s, w: w_attention(t, tm, s, w, False, 1024),
+    "histogram": w_histogram, "cumsum": w_cumsum,
+}
+
+
+def cpu_baseline(budget_s=12.0):
+    """The oracle interpreter (1 core) on a bounded sample of softmax rows."""
+    import numpy as np
+    from examples.softmax import softmax_kernel
+    from oracle import interpreter as O
+    M, N = 4096, 8192
+    x = np.random.default_rng(0).standard_normal((M, N), dtype=np.float32)
+    out = np.empty_like(x)
+    rows = 0
+    t0 = time.perf_counter()
+    order = np.random.default_rng(1).permutation(M)
+    while time.perf_counter() - t0 < budget_s and rows < M:
+        O.run_grid(softmax_kernel, (M,), out, x, N, N, N, BLOCK=8192,
+                   programs=[(int(order[rows]),)])
+        rows += 1
+    dt = time.perf_counter() - t0
+    gbps = rows * N * 4 * 2 / dt / 1e9
+    return {"value": gbps, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{rows} random rows of the fp32 [4096, 8192] softmax through the "
+                      f"oracle interpreter in {dt:.1f} s (programs are independent)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=40)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--only", default="")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only; multi-GPU runs are out "
+                          "of scope (every config shards with no exchange; see DESIGN.md)"}))
+        sys.exit(2)
+    import torch
+    torch.cuda.init()
+    from enceladus_amd.runtime import hip
+    info = hip.device_info(0)
+    log(f"device: {info.name.decode()} {info.arch.decode()} CUs={info.compute_units}")
+    timer = Timer(torch)
+    names = [n for n in (args.only.split(",") if args.only else WORKLOADS)]
+    results = {}
+    for n in names:
+        log(f"[bench] {n} ...")
+        r = WORKLOADS[n](torch, timer, args.steps, args.warmup)
+        if r["bound"] == "hbm":
+            r["roofline_frac"] = r["gbps"] * 1e9 / HBM_PEAK
+        else:
+            r["roofline_frac"] = r["tflops"] * 1e12 / MFMA_PEAK_F16
+        results[n] = r
+        log(f"[bench] {n}: {r['ms'] * 1e3:.1f} us  " +
+            (f"{r['gbps']:.0f} GB/s" if "gbps" in r else f"{r['tflops']:.1f} TFLOP/s") +
+            f"  ({100 * r['roofline_frac']:.1f}% of roofline)")
+    head = results.get("softmax") or next(iter(results.values()))
+    line = {
+        "metric": "matmul/flash-attn TFLOP/s, softmax GB/s, % of MI355X roofline",
+        "value": round(head.get("gbps", head.get("tflops", 0.0)), 2),
+        "unit": "GB/s" if "gbps" in head else "TFLOP/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(head["ms"], 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+        "config": {"workload": f"{head['name']} {head['config']}",
+                   "device": info.name.decode(), "arch": info.arch.decode(),
+                   "cus": info.compute_units},
+        "roofline": {"bound": head["bound"], "achieved": round(head.get("gbps", 0.0), 1),
+                     "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": round(head["roofline_frac"], 4), "traffic": None},
+        "workloads": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
+                          for kk, vv in v.items()} for k, v in results.items()},
+    }
+    if not args.no_cpu_baseline:
+        log("[bench] cpu baseline (oracle interpreter, bounded sample) ...")
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,1505 @@
+"""Tile IR → HIP C++ for gfx950.
+
+Every tile value lives in per-thread register arrays laid out by a wave64 `Layout`.
+Values fall in four kinds:
+
+- scalar:   a uniform C++ variable;
+- cheap:    a pure function of element coordinates (aranges, splats, index math), emitted
+            inline in whatever layout a consumer asks for, so it never moves;
+- view:     broadcast / expand_dims / trans of a stored value: a register re-indexing;
+- anchored: a register array with a fixed layout (loads, dots, reductions, scans,
+            elementwise results of anchored values, loop-carried values).
+
+A consumer that needs an anchored value in another layout gets it through an LDS round
+trip (vectorised where both sides allow). Conversions of loop-invariant values are hoisted
+in front of the loop. Reductions use in-register trees, DPP/ds_bpermute butterflies over
+lane bits and an LDS step over warp bits; scans use a serial-then-wave-then-block scheme;
+`tl.dot` lowers onto gfx950 MFMA instructions with operand layouts built for them.
+
+Reference structure: the MSL emitter `_Codegen` (reference: src/enceladus/compiler/codegen/
+msl.py:220-1381), `emit_dot` (dot.py:170-307), `emit_reduce` (reduce.py:58-194), `emit_scan`
+(scan.py:348-375) and `emit_atomic` (atomic.py:138-177). The kernel ABI keeps the
+reference's rules (runtime args in declaration order with constexprs removed, msl.py:1298-
+1342) in HIP form: one kernarg struct with natural alignment, block = num_warps*64.
+"""
+
+from __future__ import annotations
+
+import math
+import struct
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from enceladus_amd.compiler import ir
+from enceladus_amd.compiler import layout as LY
+from enceladus_amd.compiler.axis_info import AxisAnalysis
+from enceladus_amd.compiler.errors import CompilationError
+from enceladus_amd.language import core
+
+MAX_LDS = 160 * 1024
+
+_MATH = {"exp": "expf", "exp2": "exp2f", "log": "logf", "log2": "log2f", "sqrt": "sqrtf",
+         "sin": "sinf", "cos": "cosf", "tanh": "tanhf", "erf": "erff", "floor": "floorf",
+         "ceil": "ceilf"}
+_INFIX = {"add": "+", "sub": "-", "mul": "*", "div": "/", "and": "&", "or": "|", "xor": "^",
+          "eq": "==", "ne": "!=", "lt": "<", "le": "<=", "gt": ">", "ge": ">="}
+
+
+def ctype(dt: core.dtype) -> str:
+    return dt.cname
+
+
+def is_half(dt: core.dtype) -> bool:
+    return dt in (core.float16, core.bfloat16)
+
+
+def literal(v, dt: core.dtype) -> str:
+    if dt.is_bool():
+        return "true" if v else "false"
+    if dt.is_floating():
+        f = float(v)
+        if dt is core.bfloat16:
+            bits = int(np.array([f], np.float32).view(np.uint32)[0])
+            if (bits & 0x7FFFFFFF) > 0x7F800000:
+                b16 = (bits >> 16) | 0x40
+            else:
+                b16 = ((bits + 0x7FFF + ((bits >> 16) & 1)) >> 16) & 0xFFFF
+            return f"ek::bf16{{0x{b16:04x}}}"
+        if dt is core.float16:
+            f = float(np.float16(f))
+        else:
+            f = float(np.float32(f))
+        if math.isnan(f):
+            s = "__builtin_nanf(\"\")"
+        elif math.isinf(f):
+            s = "__builtin_inff()" if f > 0 else "(-__builtin_inff())"
+        else:
+            s = f.hex() + "f"
+        return f"(_Float16)({s})" if dt is core.float16 else s
+    v = int(v)
+    if dt.is_signed():
+        if dt.primitive_bitwidth == 64:
+            return f"(int64_t)({v}LL)" if v > -(1 << 63) else "(int64_t)(-9223372036854775807LL-1)"
+        if v == -(1 << 31):
+            return "(int32_t)(-2147483647-1)"
+        return f"({ctype(dt)})({v})"
+    return f"({ctype(dt)})({v}ULL)"
+
+
+def bits_expr(r: str, pairs: list[tuple[int, int]]) -> str:
+    """OR of ((r >> j) & 1) << i over (j, i) pairs, merging runs."""
+    if not pairs:
+        return "0"
+    pairs = sorted(pairs)
+    runs = []
+    for j, i in pairs:
+        if runs and runs[-1][0] + runs[-1][2] == j and runs[-1][1] + runs[-1][2] == i:
+            runs[-1][2] += 1
+        else:
+            runs.append([j, i, 1])
+    terms = []
+    for j, i, n in runs:
+        mask = (1 << n) - 1
+        t = f"({r})" if j == 0 else f"(({r}) >> {j})"
+        t = f"({t} & {mask})"
+        if i:
+            t = f"({t} << {i})"
+        terms.append(t)
+    return " | ".join(terms) if len(terms) > 1 else terms[0]
+
+
+@dataclass
+class Scope:
+    level: int
+    items: list = field(default_factory=list)
+    memo: dict = field(default_factory=dict)
+    hoist: list | None = None
+    indent: str = "  "
+
+
+@dataclass
+class KernelArg:
+    name: str
+    kind: str          # "ptr" | "scalar"
+    dtype: core.dtype
+    cparam: str        # C++ parameter type
+
+
+@dataclass
+class GeneratedKernel:
+    name: str
+    source: str
+    args: list
+    num_warps: int
+    lds_bytes: int
+    block: int
+    coarsen: int = 1
+
+
+class Emitter:
+    def __init__(self, fn: ir.Func, options: dict | None = None):
+        self.fn = fn
+        self.opt = options or {}
+        self.nw = fn.num_warps
+        self.nt = 64 * self.nw
+        self.axis = AxisAnalysis(fn)
+        self.kind: dict[int, str] = {}
+        self.lay: dict[int, LY.Layout] = {}
+        self.name: dict[int, str] = {}
+        self.vals: dict[int, ir.Value] = {}
+        self.uses: dict[int, list] = {}
+        self.def_level: dict[int, int] = {}
+        self.desc: dict[int, dict] = {}
+        self.tc: dict[tuple, str] = {}
+        self.prologue: list[str] = []
+        self.scopes = [Scope(0)]
+        self.counter = 0
+        self.lds = 0
+        self.dot_plans: dict[int, LY.DotPlan] = {}
+        self.inplace: set[int] = set()
+
+    # ------------------------------------------------------------------ utilities
+    def fresh(self, hint="v") -> str:
+        self.counter += 1
+        return f"{hint}{self.counter}"
+
+    @property
+    def cur(self) -> Scope:
+        return self.scopes[-1]
+
+    def emit(self, line: str):
+        self.cur.items.append(self.cur.indent + line)
+
+    def need_lds(self, nbytes: int):
+        self.lds = max(self.lds, nbytes)
+
+    def tile(self, v: ir.Value) -> bool:
+        return not isinstance(v.type, ir.DescType) and v.type.shape != ()
+
+    def count_uses(self, block: ir.Block):
+        for op in block.ops:
+            for o in op.operands:
+                self.uses.setdefault(o.id, []).append(op)
+            for r in op.regions:
+                self.count_uses(r)
+
+    # ------------------------------------------------------------------ layouts
+    def default_layout(self, v: ir.Value) -> LY.Layout:
+        es = 8 if v.type.ptr else v.type.dtype.itemsize
+        return LY.default_blocked(v.type.shape, self.nw, es)
+
+    def mem_layout(self, ptr: ir.Value) -> LY.Layout:
+        shape = ptr.type.shape
+        info = self.axis.get(ptr)
+        es = ptr.type.dtype.itemsize
+        best = len(shape) - 1
+        for d in range(len(shape)):
+            if info.contig[d] > info.contig[best]:
+                best = d
+        vec = min(info.contig[best], max(1, info.div[best] // es), max(1, 16 // es),
+                  shape[best])
+        vec = 1 << LY.log2(max(1, vec))
+        order = [best] + [d for d in reversed(range(len(shape))) if d != best]
+        return LY.blocked(shape, order, vec, self.nw)
+
+    def mem_vec(self, ptr: ir.Value, lay: LY.Layout) -> int:
+        """Elements per vector access for `ptr` read in `lay` (contiguity, alignment)."""
+        info = self.axis.get(ptr)
+        es = ptr.type.dtype.itemsize
+        d, nb = lay.vec_dim_bits()
+        if not lay.reg or nb == 0:
+            return 1
+        v = min(1 << nb, info.contig[d], max(1, info.div[d] // es), max(1, 16 // es))
+        return 1 << LY.log2(max(1, v))
+
+    def lay_of(self, v: ir.Value):
+        return self.lay.get(v.id)
+
+    def assign_block(self, block: ir.Block):
+        for op in block.ops:
+            self.assign_op(op)
+
+    def _anch(self, v):
+        return self.kind.get(v.id) in ("anchored", "view")
+
+    def assign_op(self, op: ir.Op):
+        n = op.name
+        for r in op.results:
+            self.vals[r.id] = r
+        if n == "for":
+            self.assign_for(op)
+            return
+        if n == "if":
+            for reg in op.regions:
+                self.assign_block(reg)
+            ty, ey = op.regions[0].ops[-1], op.regions[1].ops[-1]
+            for res, a, b in zip(op.results, ty.operands, ey.operands):
+                if not self.tile(res):
+                    self.kind[res.id] = "scalar"
+                    continue
+                self.kind[res.id] = "anchored"
+                la = self.lay_of(a) if self._anch(a) else None
+                lb = self.lay_of(b) if self._anch(b) else None
+                self.lay[res.id] = la or lb or self.default_layout(res)
+            return
+        for reg in op.regions:
+            self.assign_block(reg)
+        if not op.results:
+            return
+        res = op.result
+        if isinstance(res.type, ir.DescType):
+            self.kind[res.id] = "desc"
+            return
+        if not self.tile(res):
+            self.kind[res.id] = "scalar"
+            return
+        if n in ("const", "arange", "splat"):
+            self.kind[res.id] = "cheap"
+        elif n in ("broadcast", "expand_dims", "trans", "hint"):
+            src = op.operands[0]
+            if not self._anch(src):
+                self.kind[res.id] = "cheap"
+            else:
+                self.kind[res.id] = "view"
+                sl = self.lay[src.id]
+                if n == "broadcast":
+                    self.lay[res.id] = sl.lift(res.type.shape)
+                elif n == "expand_dims":
+                    self.lay[res.id] = sl.expand(op.attrs["axis"])
+                elif n == "trans":
+                    self.lay[res.id] = sl.permute(op.attrs["perm"])
+                else:
+                    self.lay[res.id] = sl
+        elif n in ("binary", "unary", "cast", "select", "fma", "ptr_add", "bitcast"):
+            anch = [o for o in op.operands if self.tile(o) and self._anch(o)]
+            if not anch:
+                self.kind[res.id] = "cheap"
+            else:
+                self.kind[res.id] = "anchored"
+                pick = next((o for o in anch if self.kind[o.id] == "anchored"), anch[0])
+                self.lay[res.id] = self.lay[pick.id]
+        elif n == "load":
+            self.kind[res.id] = "anchored"
+            lay = self.mem_layout(op.operands[0])
+            us = self.uses.get(res.id, [])
+            if len(us) == 1 and us[0].name == "scan":
+                lay = LY.scan_layout(res.type.shape, us[0].attrs["axis"], self.nw)
+            self.lay[res.id] = lay
+        elif n == "desc_load":
+            self.kind[res.id] = "anchored"
+            es = res.type.dtype.itemsize
+            self.lay[res.id] = LY.blocked(res.type.shape, LY.default_order(res.type.shape),
+                                          max(1, 16 // es), self.nw)
+        elif n == "dot":
+            a, b = op.operands[0], op.operands[1]
+            try:
+                plan = LY.plan_dot(a.type.shape[0], b.type.shape[1], a.type.shape[1], self.nw,
+                                   a.type.dtype.name, self.opt.get("dot_warps"))
+            except ValueError as e:
+                raise CompilationError(str(e)) from None
+            self.dot_plans[op.result.id] = plan
+            self.kind[res.id] = "anchored"
+            self.lay[res.id] = LY.mfma_acc(plan)
+        elif n == "reduce":
+            src = op.operands[0]
+            sl = self.lay[src.id] if self._anch(src) else self.default_layout(src)
+            self.kind[res.id] = "anchored"
+            self.lay[res.id] = sl.slice(op.attrs["axis"])
+        elif n == "scan":
+            src = op.operands[0]
+            ax = op.attrs["axis"]
+            sl = self.lay[src.id] if self._anch(src) else None
+            if sl is None or not LY.scan_friendly(sl, ax):
+                sl = LY.scan_layout(src.type.shape, ax, self.nw)
+            self.kind[res.id] = "anchored"
+            self.lay[res.id] = sl
+        elif n in ("atomic_rmw", "atomic_cas"):
+            self.kind[res.id] = "anchored"
+            self.lay[res.id] = self.mem_layout(op.operands[0])
+        elif n == "reshape":
+            self.kind[res.id] = "anchored"
+            self.lay[res.id] = self.default_layout(res)
+        else:
+            raise CompilationError(f"the HIP backend doesn't lower `{n}`")
+
+    def _use_layout(self, body: ir.Block, arg: ir.Value):
+        """Layout of the first memory op that reads or writes through `arg`."""
+        frontier = {arg.id}
+        for op in ir.walk(body):
+            if op.name in ("load", "store", "atomic_rmw", "atomic_cas") and \
+                    op.operands[0].id in frontier:
+                return self.mem_layout(op.operands[0])
+            if op.name in ("ptr_add", "binary", "broadcast", "hint") and \
+                    op.operands[0].id in frontier and op.results:
+                frontier.add(op.result.id)
+        return None
+
+    def assign_for(self, op: ir.Op):
+        body = op.regions[0]
+        iv, carried = body.args[0], body.args[1:]
+        inits = op.operands[3:]
+        self.kind[iv.id] = "scalar"
+        self.vals[iv.id] = iv
+        pending = []
+        for a, i in zip(carried, inits):
+            self.vals[a.id] = a
+            if not self.tile(a):
+                self.kind[a.id] = "scalar"
+            elif self._anch(i):
+                self.kind[a.id] = "anchored"
+                self.lay[a.id] = self.lay[i.id].lift(a.type.shape) if \
+                    self.lay[i.id].shape != a.type.shape else self.lay[i.id]
+            else:
+                self.kind[a.id] = "cheap"   # provisional
+                pending.append(a)
+        for _ in range(3):
+            self.assign_block(body)
+            y = body.ops[-1]
+            changed = False
+            for a, v in zip(carried, y.operands):
+                if a in pending and self._anch(v):
+                    self.kind[a.id] = "anchored"
+                    self.lay[a.id] = self.lay[v.id]
+                    pending.remove(a)
+                    changed = True
+            if not changed:
+                break
+        for a in list(pending):
+            lay = self._use_layout(body, a) or self.default_layout(a)
+            self.kind[a.id] = "anchored"
+            self.lay[a.id] = lay
+            pending.remove(a)
+        self.assign_block(body)
+        for r, a in zip(op.results, carried):
+            self.vals[r.id] = r
+            self.kind[r.id] = self.kind[a.id]
+            if a.id in self.lay:
+                self.lay[r.id] = self.lay[a.id]
+
+    # ------------------------------------------------------------------ coordinates
+    def thread_coord(self, lay: LY.Layout, d: int) -> str:
+        key = (lay.key(), d)
+        nm = self.tc.get(key)
+        if nm is not None:
+            return nm
+        pairs_l = [(i, b[1]) for i, b in enumerate(lay.lane) if b is not None and b[0] == d]
+        pairs_w = [(i, b[1]) for i, b in enumerate(lay.warp) if b is not None and b[0] == d]
+        terms = []
+        if pairs_l:
+            terms.append(bits_expr("ek_lane", pairs_l))
+        if pairs_w:
+            terms.append(bits_expr("ek_warp", pairs_w))
+        if not terms:
+            self.tc[key] = "0"
+            return "0"
+        nm = f"tc{len(self.tc)}"
+        self.prologue.append(f"  const int {nm} = {' | '.join(terms)};")
+        self.tc[key] = nm
+        return nm
+
+    def reg_coord(self, lay: LY.Layout, d: int, r: str) -> str:
+        pairs = [(i, b[1]) for i, b in enumerate(lay.reg) if b[0] == d]
+        return bits_expr(r, pairs) if pairs else "0"
+
+    def coord(self, lay: LY.Layout, d: int, r: str) -> str:
+        t = self.thread_coord(lay, d)
+        rc = self.reg_coord(lay, d, r)
+        if t == "0":
+            return f"({rc})"
+        if rc == "0":
+            return t
+        return f"({t} + ({rc}))"
+
+    def owner_cond(self, lay: LY.Layout) -> str | None:
+        lm = sum(1 << i for i, b in enumerate(lay.lane) if b is None)
+        wm = sum(1 << i for i, b in enumerate(lay.warp) if b is None)
+        conds = []
+        if lm:
+            conds.append(f"((ek_lane & {lm}) == 0)")
+        if wm:
+            conds.append(f"((ek_warp & {wm}) == 0)")
+        return " && ".join(conds) if conds else None
+
+    # ------------------------------------------------------------------ expressions
+    def ew(self, op: ir.Op, xs: list[str]) -> str:
+        """Elementwise expression of `op` given operand expressions."""
+        n = op.name
+        rt = op.result.type.dtype
+        if n == "binary":
+            k = op.attrs["op"]
+            dt = op.operands[0].type.dtype
+            a, b = xs
+            if is_half(dt):
+                a, b = f"ek::f32({a})", f"ek::f32({b})"
+            if k in ("eq", "ne", "lt", "le", "gt", "ge"):
+                return f"({a} {_INFIX[k]} {b})"
+            cdt = "float" if is_half(dt) else ctype(dt)
+            if k in ("add", "sub", "mul", "div"):
+                e = f"({a} {_INFIX[k]} {b})"
+            elif k in ("and", "or", "xor"):
+                e = f"({a} {_INFIX[k]} {b})"
+            elif k == "floordiv":
+                e = f"ek::idiv<{cdt}>({a}, {b})"
+            elif k == "mod":
+                e = f"ek::fmodf_({a}, {b})" if dt.is_floating() else f"ek::imod<{cdt}>({a}, {b})"
+            elif k == "shl":
+                e = f"ek::ishl<{cdt}>({a}, {b})"
+            elif k == "shr":
+                e = f"ek::ishr<{cdt}>({a}, {b})"
+            elif k == "min":
+                e = f"__builtin_fminf({a}, {b})" if dt.is_floating() else \
+                    f"ek::Min::op<{cdt}>({a}, {b})"
+            elif k == "max":
+                e = f"__builtin_fmaxf({a}, {b})" if dt.is_floating() else \
+                    f"ek::Max::op<{cdt}>({a}, {b})"
+            else:
+                raise CompilationError(f"unknown binary op {k}")
+            if is_half(dt):
+                return f"ek::rnd<{ctype(rt)}>({e})"
+            return f"(({ctype(rt)}){e})"
+        if n == "unary":
+            k = op.attrs["op"]
+            dt = op.operands[0].type.dtype
+            (a,) = xs
+            if k == "not":
+                return f"(!{a})" if dt.is_bool() else f"(({ctype(dt)})~{a})"
+            if dt.is_floating():
+                fa = f"ek::f32({a})" if is_half(dt) else a
+                if k == "neg":
+                    e = f"(-{fa})"
+                elif k == "abs":
+                    e = f"__builtin_fabsf({fa})"
+                elif k == "rsqrt":
+                    e = f"(1.0f / sqrtf({fa}))"
+                elif k == "sigmoid":
+                    e = f"(1.0f / (1.0f + expf(-{fa})))"
+                else:
+                    e = f"{_MATH[k]}({fa})"
+                return f"ek::rnd<{ctype(dt)}>({e})" if is_half(dt) else e
+            if k == "neg":
+                return f"(({ctype(dt)})(-{a}))"
+            if k == "abs":
+                return f"(({ctype(dt)})({a} < 0 ? -{a} : {a}))"
+            raise CompilationError(f"`{k}` needs a floating-point input")
+        if n == "cast":
+            return f"ek::cvt<{ctype(rt)}>({xs[0]})"
+        if n == "bitcast":
+            return f"__builtin_bit_cast({ctype(rt)}, {xs[0]})"
+        if n == "select":
+            return f"({xs[0]} ? {xs[1]} : {xs[2]})"
+        if n == "fma":
+            if is_half(rt):
+                return f"ek::rnd<{ctype(rt)}>(__builtin_fmaf(ek::f32({xs[0]}), ek::f32({xs[1]}), " \
+                       f"ek::f32({xs[2]})))"
+            return f"__builtin_fmaf({xs[0]}, {xs[1]}, {xs[2]})"
+        if n == "ptr_add":
+            return f"({xs[0]} + {xs[1]})"
+        raise CompilationError(f"not an elementwise op: {n}")
+
+    def cheap(self, v: ir.Value, coords: list[str]) -> str:
+        k = self.kind.get(v.id)
+        if k == "scalar":
+            return self.name[v.id]
+        op = v.op
+        if op is None:
+            raise CompilationError("internal: cheap block argument")
+        n = op.name
+        if n == "const":
+            return literal(op.attrs["value"], v.type.dtype)
+        if n == "arange":
+            s = op.attrs["start"]
+            return f"((int32_t)({s} + {coords[0]}))" if s else f"((int32_t){coords[0]})"
+        if n == "splat":
+            return self.name[op.operands[0].id]
+        if n == "broadcast":
+            x = op.operands[0]
+            xc = [("0" if x.type.shape[d] == 1 else coords[d]) for d in range(len(coords))]
+            return self.cheap(x, xc)
+        if n == "expand_dims":
+            ax = op.attrs["axis"]
+            return self.cheap(op.operands[0], coords[:ax] + coords[ax + 1:])
+        if n == "trans":
+            perm = op.attrs["perm"]
+            xc = [None] * len(perm)
+            for i, p in enumerate(perm):
+                xc[p] = coords[i]
+            return self.cheap(op.operands[0], xc)
+        if n == "hint":
+            return self.cheap(op.operands[0], coords)
+        xs = []
+        for o in op.operands:
+            xs.append(self.name[o.id] if not self.tile(o) else self.cheap(o, coords))
+        return self.ew(op, xs)
+
+    def resolve(self, v: ir.Value, lay: LY.Layout, r: str):
+        """Follows views back to a stored value: (src, layout over src shape, index expr)."""
+        while self.kind.get(v.id) == "view":
+            op = v.op
+            src = op.operands[0]
+            if op.name == "broadcast":
+                proj = lay.project(src.type.shape)
+                kept = [j for j, b in enumerate(lay.reg) if src.type.shape[b[0]] != 1]
+                r = bits_expr(r, [(j, t) for t, j in enumerate(kept)])
+                lay = proj
+            elif op.name == "expand_dims":
+                ax = op.attrs["axis"]
+                lay = lay._map(lambda b: (b[0] - (b[0] > ax), b[1]),
+                               lay.shape[:ax] + lay.shape[ax + 1:])
+            elif op.name == "trans":
+                perm = op.attrs["perm"]
+                inv = [0] * len(perm)
+                for i, p in enumerate(perm):
+                    inv[p] = i
+                lay = lay.permute(tuple(inv))
+            v = src
+        return v, lay, r
+
+    def elem(self, v: ir.Value, lay: LY.Layout, r: str) -> str:
+        k = self.kind.get(v.id)
+        if k == "scalar":
+            return self.name[v.id]
+        if k == "cheap":
+            return self.cheap(v, [self.coord(lay, d, r) for d in range(len(lay.shape))])
+        src, sl, ri = self.resolve(v, lay, r)
+        if self.kind.get(src.id) == "cheap":
+            return self.cheap(src, [self.coord(sl, d, ri) for d in range(len(sl.shape))])
+        a = self.lay[src.id]
+        nm = self.name[src.id]
+        if a.key() == sl.key():
+            return f"{nm}[{ri}]"
+        if LY.is_view(a, sl):
+            return f"{nm}[{bits_expr(ri, LY.reg_index_map(a, sl))}]"
+        conv = self.convert(src, sl)
+        return f"{conv}[{ri}]"
+
+    def array(self, v: ir.Value, lay: LY.Layout) -> str:
+        """Name of an array holding `v` in exactly `lay` (materialising if needed)."""
+        k = self.kind.get(v.id)
+        if k == "anchored" and self.lay[v.id].key() == lay.key():
+            return self.name[v.id]
+        if k in ("anchored", "view"):
+            src, sl, ri = self.resolve(v, lay, "r")
+            if self.kind.get(src.id) == "anchored" and ri == "r" and \
+                    self.lay[src.id].key() == sl.key():
+                return self.name[src.id]
+            if self.kind.get(src.id) == "anchored" and ri == "r" and \
+                    not LY.is_view(self.lay[src.id], sl):
+                return self.convert(src, sl)
+        nm = self.fresh("m")
+        t = ctype(v.type.dtype) + ("*" if v.type.ptr else "")
+        self.emit(f"{t} {nm}[{lay.nregs}];")
+        self.emit(f"#pragma unroll")
+        self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = {self.elem(v, lay, 'r')};")
+        return nm
+
+    # ------------------------------------------------------------------ LDS conversion
+    def lds_order(self, a: LY.Layout, b: LY.Layout):
+        rank = len(a.shape)
+        da, na = a.vec_dim_bits()
+        db, nb = b.vec_dim_bits()
+        f = db if nb >= na else da
+        if rank == 0:
+            return []
+        return [f] + [d for d in reversed(range(rank)) if d != f]
+
+    def lds_addr(self, shape, order, es: int):
+        """Strides (elements) for an LDS image of `shape` with the given dim order,
+        padding each fastest-dim row by 16 bytes when rows are >= 128 bytes."""
+        strides = [0] * len(shape)
+        s = 1
+        pad = 0
+        for i, d in enumerate(order):
+            strides[d] = s
+            if i == 0:
+                row = shape[d]
+                pad = (16 // es) if row * es >= 128 and len(order) > 1 else 0
+                s = row + pad
+            else:
+                s *= shape[d]
+        return strides, s
+
+    def lds_index(self, lay: LY.Layout, strides, r: str) -> str:
+        terms = []
+        for d, st in enumerate(strides):
+            if lay.shape[d] == 1:
+                continue
+            terms.append(f"({self.coord(lay, d, r)}) * {st}")
+        return " + ".join(terms) if terms else "0"
+
+    def lds_vec(self, lay: LY.Layout, order, es: int) -> int:
+        if not order or not lay.reg:
+            return 1
+        d, n = lay.vec_dim_bits()
+        if d != order[0]:
+            return 1
+        return min(1 << n, max(1, 16 // es))
+
+    def _target_scope(self, v: ir.Value) -> int:
+        return self.def_level.get(v.id, 0)
+
+    def convert(self, src: ir.Value, dst: LY.Layout) -> str:
+        key = ("conv", src.id, dst.key())
+        lvl = self._target_scope(src)
+        for s in reversed(self.scopes[lvl:]):
+            if key in s.memo:
+                return s.memo[key]
+        a = self.lay[src.id]
+        t = ctype(src.type.dtype) + ("*" if src.type.ptr else "")
+        es = 8 if src.type.ptr else src.type.dtype.itemsize
+        order = self.lds_order(a, dst)
+        strides, total = self.lds_addr(a.shape, order, es)
+        nbytes = total * es
+        if nbytes > MAX_LDS:
+            raise CompilationError(f"a layout conversion of a {a.shape} tile needs {nbytes} "
+                                   "bytes of LDS")
+        self.need_lds(nbytes)
+        nm = self.fresh("cv")
+        sname = self.name[src.id]
+        lines = []
+        wv = self.lds_vec(a, order, es)
+        rv = self.lds_vec(dst, order, es)
+        lines.append(f"{t} {nm}[{dst.nregs}];")
+        lines.append("{")
+        lines.append(f"  {t}* sm = reinterpret_cast<{t}*>(ek_smem);")
+        lines.append("  __syncthreads();")
+        lines.append("  #pragma unroll")
+        lines.append(f"  for (int r = 0; r < {a.nregs}; r += {wv}) "
+                     f"ek::vstore<{t}, {wv}>(&sm[{self.lds_index(a, strides, 'r')}], &{sname}[r]);")
+        lines.append("  __syncthreads();")
+        lines.append("  #pragma unroll")
+        lines.append(f"  for (int r = 0; r < {dst.nregs}; r += {rv}) "
+                     f"ek::vload<{t}, {rv}>(&{nm}[r], &sm[{self.lds_index(dst, strides, 'r')}]);")
+        lines.append("}")
+        self._emit_at_level(lvl, lines)
+        self.scopes[lvl].memo[key] = nm
+        return nm
+
+    def _emit_at_level(self, lvl: int, lines: list[str]):
+        if lvl >= len(self.scopes) - 1:
+            for ln in lines:
+                self.emit(ln)
+            return
+        target = self.scopes[lvl + 1].hoist
+        ind = self.scopes[lvl].indent
+        for ln in lines:
+            target.append(ind + ln)
+
+    # ------------------------------------------------------------------ scopes
+    def push_scope(self, header: str):
+        parent = self.cur
+        hoist: list[str] = []
+        parent.items.append(hoist)
+        parent.items.append(parent.indent + header)
+        s = Scope(parent.level + 1, hoist=hoist, indent=parent.indent + "  ")
+        self.scopes.append(s)
+        return s
+
+    def pop_scope(self, footer: str = "}"):
+        s = self.scopes.pop()
+        self.cur.items.append(s.items)
+        self.emit(footer)
+
+    def define(self, v: ir.Value, name: str):
+        self.name[v.id] = name
+        self.def_level[v.id] = len(self.scopes) - 1
+
+    # ------------------------------------------------------------------ ops
+    def gen_block(self, block: ir.Block):
+        for op in block.ops:
+            self.gen_op(op)
+
+    def gen_op(self, op: ir.Op):
+        n = op.name
+        fn = getattr(self, f"op_{n}", None)
+        if n in ("yield",):
+            return
+        if fn is not None:
+            fn(op)
+            return
+        if n in ("binary", "unary", "cast", "select", "fma", "ptr_add", "bitcast"):
+            self.op_elementwise(op)
+            return
+        if n in ("const", "arange", "splat", "broadcast", "expand_dims", "trans", "hint"):
+            res = op.result
+            k = self.kind.get(res.id)
+            if k == "scalar":
+                self.op_elementwise(op)
+            self.def_level[res.id] = len(self.scopes) - 1
+            return
+        raise CompilationError(f"the HIP backend doesn't lower `{n}`")
+
+    def scalar_expr(self, op: ir.Op) -> str:
+        n = op.name
+        if n == "const":
+            return literal(op.attrs["value"], op.result.type.dtype)
+        if n == "hint":
+            return self.name[op.operands[0].id]
+        xs = [self.name[o.id] for o in op.operands]
+        return self.ew(op, xs)
+
+    def op_elementwise(self, op: ir.Op):
+        res = op.result
+        k = self.kind[res.id]
+        t = ctype(res.type.dtype) + ("*" if res.type.ptr else "")
+        if k == "scalar":
+            nm = self.fresh("s")
+            self.emit(f"{t} const {nm} = {self.scalar_expr(op)};")
+            self.define(res, nm)
+            return
+        if k == "cheap":
+            self.def_level[res.id] = len(self.scopes) - 1
+            return
+        lay = self.lay[res.id]
+        nm = self.fresh("t")
+        xs = [self.elem(o, lay, "r") if self.tile(o) else self.name[o.id] for o in op.operands]
+        self.emit(f"{t} {nm}[{lay.nregs}];")
+        self.emit("#pragma unroll")
+        self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = {self.ew(op, xs)};")
+        self.define(res, nm)
+
+    def op_program_id(self, op):
+        nm = self.fresh("pid")
+        ax = "xyz"[op.attrs["axis"]]
+        src = f"ek_pid_{ax}" if self.opt.get("_coarsen") else f"(int32_t)blockIdx.{ax}"
+        self.emit(f"const int32_t {nm} = {src};")
+        self.define(op.result, nm)
+
+    def op_num_programs(self, op):
+        nm = self.fresh("np")
+        ax = "xyz"[op.attrs["axis"]]
+        src = f"ek_np_{ax}" if self.opt.get("_coarsen") else f"(int32_t)gridDim.{ax}"
+        self.emit(f"const int32_t {nm} = {src};")
+        self.define(op.result, nm)
+
+    def op_barrier(self, op):
+        self.emit("__syncthreads();")
+
+    # -- memory ----------------------------------------------------------------------
+    def op_load(self, op):
+        res = op.result
+        ptr = op.operands[0]
+        t = ctype(res.type.dtype)
+        if not self.tile(res):
+            nm = self.fresh("s")
+            p = self.name[ptr.id]
+            if len(op.operands) > 1:
+                m, o = self.name[op.operands[1].id], self.name[op.operands[2].id]
+                self.emit(f"const {t} {nm} = {m} ? *{p} : {o};")
+            else:
+                self.emit(f"const {t} {nm} = *{p};")
+            self.define(res, nm)
+            return
+        lay = self.lay[res.id]
+        V = self.mem_vec(ptr, lay)
+        nm = self.fresh("ld")
+        self.emit(f"{t} {nm}[{lay.nregs}];")
+        self.emit("#pragma unroll")
+        hdr = f"for (int rv = 0; rv < {lay.nregs}; rv += {V}) {{"
+        self.emit(hdr)
+        pe = lambda i: self.elem(ptr, lay, f"rv + {i}" if i else "rv")  # noqa: E731
+        if len(op.operands) == 1:
+            self.emit(f"  ek::vload<{t}, {V}>(&{nm}[rv], {pe(0)});")
+        else:
+            mask, other = op.operands[1], op.operands[2]
+            me = lambda i: self.elem(mask, lay, f"rv + {i}" if i else "rv")  # noqa: E731
+            oe = lambda i: self.elem(other, lay, f"rv + {i}" if i else "rv")  # noqa: E731
+            if V > 1:
+                allm = " && ".join(f"({me(i)})" for i in range(V))
+                self.emit(f"  if ({allm}) {{ ek::vload<{t}, {V}>(&{nm}[rv], {pe(0)}); }}")
+                self.emit("  else {")
+                for i in range(V):
+                    self.emit(f"    {nm}[rv + {i}] = ({me(i)}) ? *({pe(i)}) : {oe(i)};")
+                self.emit("  }")
+            else:
+                self.emit(f"  {nm}[rv] = ({me(0)}) ? *({pe(0)}) : {oe(0)};")
+        self.emit("}")
+        self.define(res, nm)
+
+    def op_store(self, op):
+        ptr, val = op.operands[0], op.operands[1]
+        mask = op.operands[2] if len(op.operands) > 2 else None
+        t = ctype(val.type.dtype)
+        if not self.tile(ptr):
+            cond = "ek_tid == 0" + (f" && {self.name[mask.id]}" if mask is not None else "")
+            self.emit(f"if ({cond}) *{self.name[ptr.id]} = {self.name[val.id]};")
+            return
+        lay = self.mem_layout(ptr)
+        if self._anch(val) and self.kind[val.id] == "anchored":
+            vl = self.lay[val.id]
+            want = self.mem_vec(ptr, lay)
+            if vl.shape == lay.shape and self.mem_vec(ptr, vl) >= want:
+                lay = vl
+        V = self.mem_vec(ptr, lay)
+        own = self.owner_cond(lay)
+        pe = lambda i: self.elem(ptr, lay, f"rv + {i}" if i else "rv")  # noqa: E731
+        vals = self.array(val, lay)
+        if own:
+            self.emit(f"if ({own}) {{")
+        self.emit("#pragma unroll")
+        self.emit(f"for (int rv = 0; rv < {lay.nregs}; rv += {V}) {{")
+        if mask is None:
+            self.emit(f"  ek::vstore<{t}, {V}>({pe(0)}, &{vals}[rv]);")
+        else:
+            me = lambda i: self.elem(mask, lay, f"rv + {i}" if i else "rv")  # noqa: E731
+            if V > 1:
+                allm = " && ".join(f"({me(i)})" for i in range(V))
+                self.emit(f"  if ({allm}) {{ ek::vstore<{t}, {V}>({pe(0)}, &{vals}[rv]); }}")
+                self.emit("  else {")
+                for i in range(V):
+                    self.emit(f"    if ({me(i)}) *({pe(i)}) = {vals}[rv + {i}];")
+                self.emit("  }")
+            else:
+                self.emit(f"  if ({me(0)}) *({pe(0)}) = {vals}[rv];")
+        self.emit("}")
+        if own:
+            self.emit("}")
+
+    def op_make_desc(self, op):
+        base = op.operands[0]
+        vals = [self.name[o.id] for o in op.operands[1:]]
+        rank = op.result.type.rank
+        info = {"base": self.name[base.id], "shape": vals[:rank], "strides": vals[rank:],
+                "base_v": base, "shape_v": op.operands[1:1 + rank],
+                "stride_v": op.operands[1 + rank:]}
+        self.desc[op.result.id] = info
+        self.def_level[op.result.id] = len(self.scopes) - 1
+
+    def _desc_vec(self, d: dict, offs: list[ir.Value], lay: LY.Layout, es: int) -> int:
+        """Vector width for a descriptor block access in `lay` (contiguous last dim)."""
+        dvec, nb = lay.vec_dim_bits()
+        rank = len(lay.shape)
+        if dvec != rank - 1 or nb == 0:
+            return 1
+        v = min(1 << nb, max(1, 16 // es))
+        align = self.axis.get(d["base_v"]).div[0]
+        for o in offs[-1:]:
+            align = math.gcd(align, self.axis.get(o).div[0] * es)
+        for s in d["stride_v"][:-1]:
+            align = math.gcd(align, self.axis.get(s).div[0] * es)
+        v = min(v, max(1, align // es))
+        return 1 << LY.log2(max(1, v))
+
+    def _desc_addr(self, d, offs, lay, r):
+        rank = len(lay.shape)
+        idx = []
+        conds = []
+        for k in range(rank):
+            c = f"({self.name[offs[k].id]} + {self.coord(lay, k, r)})"
+            conds.append(f"((unsigned){c} < (unsigned){d['shape'][k]})")
+            idx.append(c if k == rank - 1 else f"{c} * {d['strides'][k]}")
+        return " + ".join(idx), " && ".join(conds)
+
+    def op_desc_load(self, op):
+        desc, offs = op.operands[0], op.operands[1:]
+        d = self.desc[desc.id]
+        res = op.result
+        lay = self.lay[res.id]
+        t = ctype(res.type.dtype)
+        es = res.type.dtype.itemsize
+        V = self._desc_vec(d, offs, lay, es)
+        nm = self.fresh("dl")
+        self.emit(f"{t} {nm}[{lay.nregs}];")
+        self.emit("#pragma unroll")
+        self.emit(f"for (int rv = 0; rv < {lay.nregs}; rv += {V}) {{")
+        addr, cond = self._desc_addr(d, offs, lay, "rv")
+        zero = literal(0, res.type.dtype)
+        if V > 1:
+            _, cond_last = self._desc_addr(d, offs, lay, f"rv + {V - 1}")
+            self.emit(f"  if ({cond} && {cond_last}) {{ ek::vload<{t}, {V}>(&{nm}[rv], "
+                      f"{d['base']} + {addr}); }}")
+            self.emit("  else {")
+            for i in range(V):
+                a_i, c_i = self._desc_addr(d, offs, lay, f"rv + {i}")
+                self.emit(f"    {nm}[rv + {i}] = ({c_i}) ? {d['base']}[{a_i}] : {zero};")
+            self.emit("  }")
+        else:
+            self.emit(f"  {nm}[rv] = ({cond}) ? {d['base']}[{addr}] : {zero};")
+        self.emit("}")
+        self.define(res, nm)
+
+    def op_desc_store(self, op):
+        desc, offs, val = op.operands[0], op.operands[1:-1], op.operands[-1]
+        d = self.desc[desc.id]
+        t = ctype(val.type.dtype)
+        es = val.type.dtype.itemsize
+        lay = LY.blocked(val.type.shape, LY.default_order(val.type.shape), max(1, 16 // es),
+                         self.nw)
+        V = self._desc_vec(d, offs, lay, es)
+        vals = self.array(val, lay)
+        self.emit("#pragma unroll")
+        self.emit(f"for (int rv = 0; rv < {lay.nregs}; rv += {V}) {{")
+        addr, cond = self._desc_addr(d, offs, lay, "rv")
+        if V > 1:
+            _, cond_last = self._desc_addr(d, offs, lay, f"rv + {V - 1}")
+            self.emit(f"  if ({cond} && {cond_last}) {{ ek::vstore<{t}, {V}>({d['base']} + "
+                      f"{addr}, &{vals}[rv]); }}")
+            self.emit("  else {")
+            for i in range(V):
+                a_i, c_i = self._desc_addr(d, offs, lay, f"rv + {i}")
+                self.emit(f"    if ({c_i}) {d['base']}[{a_i}] = {vals}[rv + {i}];")
+            self.emit("  }")
+        else:
+            self.emit(f"  if ({cond}) {d['base']}[{addr}] = {vals}[rv];")
+        self.emit("}")
+
+    # -- atomics --------------------------------------------------------------------
+    def _atomic_call(self, kind: str, t: str, dt: core.dtype, p: str, v: str, cmp=None) -> str:
+        scope = "__ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT"
+        if kind == "add":
+            return f"__hip_atomic_fetch_add({p}, {v}, {scope})"
+        if kind in ("and", "or", "xor"):
+            return f"__hip_atomic_fetch_{kind}({p}, {v}, {scope})"
+        if kind == "xchg":
+            return f"__hip_atomic_exchange({p}, {v}, {scope})"
+        if kind in ("max", "min") and not dt.is_floating():
+            return f"__hip_atomic_fetch_{kind}({p}, {v}, {scope})"
+        if kind in ("max", "min"):
+            fnm = "__builtin_fmaxf" if kind == "max" else "__builtin_fminf"
+            return (f"([&]() {{ {t} o = __hip_atomic_load({p}, {scope}); "
+                    f"while (true) {{ {t} n = {fnm}(o, {v}); "
+                    f"if (__hip_atomic_compare_exchange_strong({p}, &o, n, __ATOMIC_RELAXED, "
+                    f"__ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break; }} return o; }})()")
+        if kind == "cas":
+            return (f"([&]() {{ {t} o = {cmp}; __hip_atomic_compare_exchange_strong({p}, &o, "
+                    f"{v}, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); "
+                    f"return o; }})()")
+        raise CompilationError(f"unknown atomic {kind}")
+
+    def op_atomic_rmw(self, op):
+        self._atomic(op, op.attrs["op"])
+
+    def op_atomic_cas(self, op):
+        self._atomic(op, "cas")
+
+    def _atomic(self, op, kind):
+        res = op.result
+        dt = res.type.dtype
+        t = ctype(dt)
+        ptr = op.operands[0]
+        used = bool(self.uses.get(res.id))
+        has_mask = op.attrs.get("has_mask")
+        if kind == "cas":
+            cmp_v, val_v = op.operands[1], op.operands[2]
+            mask = None
+        else:
+            val_v = op.operands[1]
+            cmp_v = None
+            mask = op.operands[2] if has_mask else None
+        if not self.tile(res):
+            nm = self.fresh("s")
+            p, v = self.name[ptr.id], self.name[val_v.id]
+            c = self.name[cmp_v.id] if cmp_v is not None else None
+            m = self.name[mask.id] if mask is not None else "true"
+            self.need_lds(8)
+            self.emit(f"{t} {nm};")
+            self.emit("{")
+            self.emit(f"  {t}* sm = reinterpret_cast<{t}*>(ek_smem);")
+            self.emit("  __syncthreads();")
+            self.emit(f"  if (ek_tid == 0) sm[0] = ({m}) ? {self._atomic_call(kind, t, dt, p, v, c)}"
+                      f" : ({t})0;")
+            self.emit("  __syncthreads();")
+            self.emit(f"  {nm} = sm[0];")
+            self.emit("}")
+            self.define(res, nm)
+            return
+        lay = self.lay[res.id]
+        own = self.owner_cond(lay)
+        if used and own:
+            raise CompilationError("the result of a tl.atomic_* on a tile with replicated "
+                                   "elements isn't supported; use a larger tile or fewer warps")
+        nm = self.fresh("at")
+        self.emit(f"{t} {nm}[{lay.nregs}];")
+        self.emit("#pragma unroll")
+        self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {{")
+        p = self.elem(ptr, lay, "r")
+        v = self.elem(val_v, lay, "r")
+        c = self.elem(cmp_v, lay, "r") if cmp_v is not None else None
+        conds = []
+        if own:
+            conds.append(own)
+        if mask is not None:
+            conds.append(f"({self.elem(mask, lay, 'r')})")
+        call = self._atomic_call(kind, t, dt, p, v, c)
+        if conds:
+            self.emit(f"  {nm}[r] = ({' && '.join(conds)}) ? {call} : ({t})0;")
+        else:
+            self.emit(f"  {nm}[r] = {call};")
+        self.emit("}")
+        self.define(res, nm)
+
+    # -- reshape ----------------------------------------------------------------------
+    def op_reshape(self, op):
+        src, res = op.operands[0], op.result
+        t = ctype(res.type.dtype)
+        es = res.type.dtype.itemsize
+        sl = self.lay[src.id] if self._anch(src) else self.default_layout(src)
+        arr = self.array(src, sl)
+        dst = self.lay[res.id]
+        n = res.type.numel
+        self.need_lds(n * es)
+
+        def lin(lay, r):
+            terms = []
+            s = 1
+            for d in reversed(range(len(lay.shape))):
+                terms.append(f"({self.coord(lay, d, r)}) * {s}")
+                s *= lay.shape[d]
+            return " + ".join(terms)
+        nm = self.fresh("rs")
+        self.emit(f"{t} {nm}[{dst.nregs}];")
+        self.emit("{")
+        self.emit(f"  {t}* sm = reinterpret_cast<{t}*>(ek_smem);")
+        self.emit("  __syncthreads();")
+        self.emit(f"  for (int r = 0; r < {sl.nregs}; ++r) sm[{lin(sl, 'r')}] = {arr}[r];")
+        self.emit("  __syncthreads();")
+        self.emit(f"  for (int r = 0; r < {dst.nregs}; ++r) {nm}[r] = sm[{lin(dst, 'r')}];")
+        self.emit("}")
+        self.define(res, nm)
+
+    # -- reductions -------------------------------------------------------------------
+    def op_reduce(self, op):
+        src, res = op.operands[0], op.result
+        ax = op.attrs["axis"]
+        kind = op.attrs["kind"]
+        dt = src.type.dtype
+        sl = self.lay[src.id] if self._anch(src) else self.default_layout(src)
+        if self.kind.get(src.id) == "view" or (self._anch(src) and
+                                                self.kind.get(src.id) != "anchored"):
+            sl = self.lay[src.id]
+        arr = self.array(src, sl)
+        out = sl.slice(ax)
+        acc_t = "float" if is_half(dt) else ctype(dt)
+        arg = kind in ("argmax", "argmin")
+        comb = {"sum": "ek::Sum", "max": "ek::Max", "min": "ek::Min",
+                "argmax": "ek::Max", "argmin": "ek::Min"}[kind]
+        axis_reg = [i for i, b in enumerate(sl.reg) if b[0] == ax]
+        keep_reg = [i for i, b in enumerate(sl.reg) if b[0] != ax]
+        ro_n = 1 << len(keep_reg)
+        ra_n = 1 << len(axis_reg)
+        nm = self.fresh("rd")
+        rt = ctype(res.type.dtype)
+        cvt_in = (lambda x: f"ek::f32({x})") if is_half(dt) else (lambda x: x)
+        idx_in = lambda ro, ra: " | ".join(  # noqa: E731
+            [bits_expr(ro, [(t, i) for t, i in enumerate(keep_reg)]),
+             bits_expr(ra, [(t, i) for t, i in enumerate(axis_reg)])])
+        self.emit(f"{acc_t} {nm}_v[{ro_n}];")
+        if arg:
+            self.emit(f"int32_t {nm}_i[{ro_n}];")
+        self.emit("#pragma unroll")
+        self.emit(f"for (int ro = 0; ro < {ro_n}; ++ro) {{")
+        axc = self.coord(sl, ax, idx_in("ro", "ra"))
+        first = cvt_in(arr + "[" + idx_in("ro", "0") + "]")
+        nxt = cvt_in(arr + "[" + idx_in("ro", "ra") + "]")
+        if arg:
+            self.emit(f"  {acc_t} bv = {first};")
+            self.emit(f"  int32_t bi = {axc.replace('ra', '0')};")
+            self.emit("  #pragma unroll")
+            self.emit(f"  for (int ra = 1; ra < {ra_n}; ++ra) {{")
+            self.emit(f"    {acc_t} cv = {nxt}; int32_t ci = {axc};")
+            self.emit(f"    if ({self._arg_better(kind, dt)}) {{ bv = cv; bi = ci; }}")
+            self.emit("  }")
+            self.emit(f"  {nm}_v[ro] = bv; {nm}_i[ro] = bi;")
+        else:
+            self.emit(f"  {acc_t} a = {first};")
+            self.emit("  #pragma unroll")
+            self.emit(f"  for (int ra = 1; ra < {ra_n}; ++ra) a = {comb}::op<{acc_t}>(a, {nxt});")
+            self.emit(f"  {nm}_v[ro] = a;")
+        self.emit("}")
+        # lanes
+        for i, b in enumerate(sl.lane):
+            if b is None or b[0] != ax:
+                continue
+            self.emit("#pragma unroll")
+            self.emit(f"for (int ro = 0; ro < {ro_n}; ++ro) {{")
+            if arg:
+                self.emit(f"  {acc_t} cv = ek::shfl_xor<{1 << i}>({nm}_v[ro]);"
+                          f" int32_t ci = ek::shfl_xor<{1 << i}>({nm}_i[ro]);")
+                self.emit(f"  {acc_t} bv = {nm}_v[ro]; int32_t bi = {nm}_i[ro];")
+                self.emit(f"  if ({self._arg_better(kind, dt)}) {{ {nm}_v[ro] = cv; "
+                          f"{nm}_i[ro] = ci; }}")
+            else:
+                self.emit(f"  {nm}_v[ro] = {comb}::op<{acc_t}>({nm}_v[ro], "
+                          f"ek::shfl_xor<{1 << i}>({nm}_v[ro]));")
+            self.emit("}")
+        # warps
+        wbits = [i for i, b in enumerate(sl.warp) if b is not None and b[0] == ax]
+        if wbits:
+            nwa = 1 << len(wbits)
+            nout = max(1, res.type.numel)
+            esz = 4 if acc_t in ("float", "int32_t", "uint32_t") else 8
+            per = nout * (esz + (4 if arg else 0))
+            self.need_lds(nwa * per)
+            lane_ax = sum(1 << i for i, b in enumerate(sl.lane) if b is not None and b[0] == ax)
+            widx = bits_expr("ek_warp", [(w, t) for t, w in enumerate(wbits)])
+            outlin = self._lin(out, "ro")
+            self.emit("{")
+            self.emit(f"  {acc_t}* sm = reinterpret_cast<{acc_t}*>(ek_smem);")
+            if arg:
+                self.emit(f"  int32_t* si = reinterpret_cast<int32_t*>(ek_smem + {nwa * nout * esz});")
+            self.emit("  __syncthreads();")
+            self.emit(f"  if ((ek_lane & {lane_ax}) == 0) {{")
+            self.emit("    #pragma unroll")
+            self.emit(f"    for (int ro = 0; ro < {ro_n}; ++ro) {{ sm[({widx}) * {nout} + {outlin}]"
+                      f" = {nm}_v[ro];" + (f" si[({widx}) * {nout} + {outlin}] = {nm}_i[ro];"
+                                           if arg else "") + " }")
+            self.emit("  }")
+            self.emit("  __syncthreads();")
+            self.emit("  #pragma unroll")
+            self.emit(f"  for (int ro = 0; ro < {ro_n}; ++ro) {{")
+            if arg:
+                self.emit(f"    {acc_t} bv = sm[{outlin}]; int32_t bi = si[{outlin}];")
+                self.emit(f"    for (int w = 1; w < {nwa}; ++w) {{ {acc_t} cv = sm[w * {nout} + "
+                          f"{outlin}]; int32_t ci = si[w * {nout} + {outlin}]; "
+                          f"if ({self._arg_better(kind, dt)}) {{ bv = cv; bi = ci; }} }}")
+                self.emit(f"    {nm}_v[ro] = bv; {nm}_i[ro] = bi;")
+            else:
+                self.emit(f"    {acc_t} a = sm[{outlin}];")
+                self.emit(f"    for (int w = 1; w < {nwa}; ++w) a = {comb}::op<{acc_t}>(a, "
+                          f"sm[w * {nout} + {outlin}]);")
+                self.emit(f"    {nm}_v[ro] = a;")
+            self.emit("  }")
+            self.emit("}")
+        src_arr = f"{nm}_i" if arg else f"{nm}_v"
+        fin = (lambda x: f"ek::rnd<{rt}>({x})") if is_half(res.type.dtype) else (lambda x: x)
+        if res.type.shape == ():
+            self.emit(f"const {rt} {nm} = {fin(src_arr + '[0]')};")
+        else:
+            self.emit(f"{rt} {nm}[{ro_n}];")
+            self.emit("#pragma unroll")
+            self.emit(f"for (int r = 0; r < {ro_n}; ++r) {nm}[r] = {fin(src_arr + '[r]')};")
+        self.define(res, nm)
+
+    def _arg_better(self, kind, dt) -> str:
+        gt = ">" if kind == "argmax" else "<"
+        if dt.is_floating():
+            return (f"((cv {gt} bv) || (cv == bv && ci < bi) || (bv != bv && cv == cv) || "
+                    f"(bv != bv && cv != cv && ci < bi))")
+        return f"((cv {gt} bv) || (cv == bv && ci < bi))"
+
+    def _lin(self, lay: LY.Layout, r: str) -> str:
+        if not lay.shape:
+            return "0"
+        terms = []
+        s = 1
+        for d in reversed(range(len(lay.shape))):
+            terms.append(f"({self.coord(lay, d, r)}) * {s}")
+            s *= lay.shape[d]
+        return "(" + " + ".join(terms) + ")"
+
+    # -- scans ------------------------------------------------------------------------
+    def op_scan(self, op):
+        src, res = op.operands[0], op.result
+        ax = op.attrs["axis"]
+        rev = op.attrs["reverse"]
+        lay = self.lay[res.id]
+        dt = res.type.dtype
+        acc_t = "float" if is_half(dt) else ctype(dt)
+        arr = self.array(src, lay)
+        nm = self.fresh("sc")
+        R = lay.nregs
+        k = sum(1 for b in lay.reg if b[0] == ax)
+        run = 1 << k
+        outer = R // run
+        cin = (lambda x: f"ek::f32({x})") if is_half(dt) else (lambda x: x)
+        self.emit(f"{acc_t} {nm}_x[{R}];")
+        self.emit("#pragma unroll")
+        self.emit(f"for (int r = 0; r < {R}; ++r) {nm}_x[r] = {cin(arr + '[r]')};")
+        # phase 1: serial within each run
+        self.emit("#pragma unroll")
+        self.emit(f"for (int o = 0; o < {outer}; ++o) {{")
+        self.emit("  #pragma unroll")
+        if not rev:
+            self.emit(f"  for (int i = 1; i < {run}; ++i) {nm}_x[o * {run} + i] += "
+                      f"{nm}_x[o * {run} + i - 1];")
+        else:
+            self.emit(f"  for (int i = {run - 2}; i >= 0; --i) {nm}_x[o * {run} + i] += "
+                      f"{nm}_x[o * {run} + i + 1];")
+        self.emit("}")
+        lane_bits = [i for i, b in enumerate(lay.lane) if b is not None and b[0] == ax]
+        warp_bits = [i for i, b in enumerate(lay.warp) if b is not None and b[0] == ax]
+        last = run - 1 if not rev else 0
+        if lane_bits or warp_bits:
+            self.emit(f"{acc_t} {nm}_t[{outer}], {nm}_p[{outer}];")
+            self.emit("#pragma unroll")
+            self.emit(f"for (int o = 0; o < {outer}; ++o) {{ {nm}_t[o] = {nm}_x[o * {run} + "
+                      f"{last}]; {nm}_p[o] = {nm}_t[o]; }}")
+            low = 0
+            for i in lane_bits:
+                bit = 1 << i
+                if not rev:
+                    srcl = f"((ek_lane & ~{bit}) | {low})"
+                    cond = f"(ek_lane & {bit})"
+                else:
+                    srcl = f"((ek_lane | {bit}) & ~{low})"
+                    cond = f"!(ek_lane & {bit})"
+                self.emit("#pragma unroll")
+                self.emit(f"for (int o = 0; o < {outer}; ++o) {{ {acc_t} u = ek::shfl({nm}_p[o], "
+                          f"{srcl}); if ({cond}) {nm}_p[o] += u; }}")
+                low |= bit
+            # warp totals through LDS
+            if warp_bits:
+                nwa = 1 << len(warp_bits)
+                rows = res.type.numel // res.type.shape[ax]
+                esz = 8 if acc_t in ("int64_t", "uint64_t") else 4
+                self.need_lds(nwa * rows * esz)
+                widx = bits_expr("ek_warp", [(w, t) for t, w in enumerate(warp_bits)])
+                lane_ax = sum(1 << i for i in lane_bits)
+                rowc = self._row_lin(lay, ax, f"o * {run}")
+                writer = f"(ek_lane & {lane_ax}) == {lane_ax if not rev else 0}"
+                self.emit("{")
+                self.emit(f"  {acc_t}* sm = reinterpret_cast<{acc_t}*>(ek_smem);")
+                self.emit("  __syncthreads();")
+                self.emit(f"  if ({writer}) {{")
+                self.emit("    #pragma unroll")
+                self.emit(f"    for (int o = 0; o < {outer}; ++o) sm[({widx}) * {rows} + {rowc}]"
+                          f" = {nm}_p[o];")
+                self.emit("  }")
+                self.emit("  __syncthreads();")
+                self.emit(f"  const int ek_wa = {widx};")
+                self.emit("  #pragma unroll")
+                self.emit(f"  for (int o = 0; o < {outer}; ++o) {{")
+                self.emit(f"    {acc_t} s = 0;")
+                if not rev:
+                    self.emit(f"    for (int w = 0; w < ek_wa; ++w) s += sm[w * {rows} + {rowc}];")
+                else:
+                    self.emit(f"    for (int w = ek_wa + 1; w < {nwa}; ++w) s += sm[w * {rows} + "
+                              f"{rowc}];")
+                self.emit(f"    {nm}_p[o] += s;")
+                self.emit("  }")
+                self.emit("}")
+            self.emit("#pragma unroll")
+            self.emit(f"for (int o = 0; o < {outer}; ++o) {{ {acc_t} e = {nm}_p[o] - {nm}_t[o];")
+            self.emit("  #pragma unroll")
+            self.emit(f"  for (int i = 0; i < {run}; ++i) {nm}_x[o * {run} + i] += e; }}")
+        rt = ctype(dt)
+        fin = (lambda x: f"ek::rnd<{rt}>({x})") if is_half(dt) else (lambda x: x)
+        self.emit(f"{rt} {nm}[{R}];")
+        self.emit("#pragma unroll")
+        self.emit(f"for (int r = 0; r < {R}; ++r) {nm}[r] = {fin(nm + '_x[r]')};")
+        self.define(res, nm)
+
+    def _row_lin(self, lay: LY.Layout, ax: int, r: str) -> str:
+        terms = []
+        s = 1
+        for d in reversed(range(len(lay.shape))):
+            if d == ax:
+                continue
+            terms.append(f"({self.coord(lay, d, r)}) * {s}")
+            s *= lay.shape[d]
+        return "(" + " + ".join(terms) + ")" if terms else "0"
+
+    # -- dot --------------------------------------------------------------------------
+    def op_dot(self, op):
+        a, b, c = op.operands
+        res = op.result
+        plan = self.dot_plans[res.id]
+        la, lb = LY.mfma_operand(plan, "a"), LY.mfma_operand(plan, "b")
+        lc = self.lay[res.id]
+        ins = plan.inst
+        aa = self.array(a, la)
+        bb = self.array(b, lb)
+        cdt = res.type.dtype
+        nacc = 16 if ins.m == 32 else 4
+        single = len(self.uses.get(c.id, [])) == 1
+        if cdt is core.float32 and self.kind.get(c.id) == "anchored" and single and \
+                self.lay[c.id].key() == lc.key():
+            nm = self.name[c.id]
+        else:
+            nm = self.fresh("acc")
+            self.emit(f"float {nm}[{lc.nregs}];")
+            self.emit("#pragma unroll")
+            self.emit(f"for (int r = 0; r < {lc.nregs}; ++r) {nm}[r] = "
+                      f"ek::f32({self.elem(c, lc, 'r')});")
+        tm, tn, tk, kpl = plan.tm, plan.tn, plan.tk, ins.kpl
+        self.emit("#pragma unroll")
+        self.emit(f"for (int kk = 0; kk < {tk}; ++kk) {{")
+        self.emit("  #pragma unroll")
+        self.emit(f"  for (int im = 0; im < {tm}; ++im) {{")
+        self.emit("    #pragma unroll")
+        self.emit(f"    for (int in_ = 0; in_ < {tn}; ++in_) ek::{ins.fn}(&{nm}[(im * {tn} + in_) "
+                  f"* {nacc}], &{aa}[(im * {tk} + kk) * {kpl}], &{bb}[(in_ * {tk} + kk) * {kpl}]);")
+        self.emit("  }")
+        self.emit("}")
+        if cdt is not core.float32:
+            out = self.fresh("acch")
+            self.emit(f"{ctype(cdt)} {out}[{lc.nregs}];")
+            self.emit(f"for (int r = 0; r < {lc.nregs}; ++r) {out}[r] = ek::rnd<{ctype(cdt)}>"
+                      f"({nm}[r]);")
+            nm = out
+        self.define(res, nm)
+
+    # -- control flow -----------------------------------------------------------------
+    def op_for(self, op):
+        body = op.regions[0]
+        iv, carried = body.args[0], body.args[1:]
+        lo, hi, step = (self.name[o.id] for o in op.operands[:3])
+        inits = op.operands[3:]
+        names = []
+        for a, i in zip(carried, inits):
+            t = ctype(a.type.dtype) + ("*" if a.type.ptr else "")
+            nm = self.fresh("c")
+            names.append(nm)
+            if not self.tile(a):
+                self.emit(f"{t} {nm} = {self.name[i.id]};")
+            else:
+                lay = self.lay[a.id]
+                self.emit(f"{t} {nm}[{lay.nregs}];")
+                self.emit("#pragma unroll")
+                self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = "
+                          f"{self.elem(i, lay, 'r')};")
+        it = ctype(iv.type.dtype)
+        ivn = self.fresh("iv")
+        self.push_scope(f"for ({it} {ivn} = {lo}; {ivn} < {hi}; {ivn} += {step}) {{")
+        self.define(iv, ivn)
+        for a, nm in zip(carried, names):
+            self.define(a, nm)
+        self.gen_block(body)
+        y = body.ops[-1]
+        self._assign_yield(y.operands, carried, names)
+        self.pop_scope()
+        for r, nm in zip(op.results, names):
+            self.define(r, nm)
+
+    def _assign_yield(self, vals, targets, names):
+        tids = {t.id for t in targets}
+        need_tmp = False
+        for v in vals:
+            s = v
+            if self.kind.get(v.id) == "view":
+                s, _, _ = self.resolve(v, self.lay[v.id], "r")
+            if s.id in tids:
+                need_tmp = True
+        pend = []
+        for v, t, nm in zip(vals, targets, names):
+            if v.id == t.id:
+                continue
+            if not self.tile(t):
+                if need_tmp:
+                    tmp = self.fresh("y")
+                    self.emit(f"const {ctype(t.type.dtype)}{'*' if t.type.ptr else ''} {tmp} = "
+                              f"{self.name[v.id]};")
+                    pend.append((nm, tmp, None))
+                else:
+                    self.emit(f"{nm} = {self.name[v.id]};")
+                continue
+            lay = self.lay[t.id]
+            if self.kind.get(v.id) == "anchored" and self.name.get(v.id) == nm:
+                continue
+            if need_tmp:
+                tmp = self.fresh("y")
+                tt = ctype(t.type.dtype) + ("*" if t.type.ptr else "")
+                self.emit(f"{tt} {tmp}[{lay.nregs}];")
+                self.emit("#pragma unroll")
+                self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {tmp}[r] = "
+                          f"{self.elem(v, lay, 'r')};")
+                pend.append((nm, tmp, lay.nregs))
+            else:
+                self.emit("#pragma unroll")
+                self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = "
+                          f"{self.elem(v, lay, 'r')};")
+        for nm, tmp, n in pend:
+            if n is None:
+                self.emit(f"{nm} = {tmp};")
+            else:
+                self.emit("#pragma unroll")
+                self.emit(f"for (int r = 0; r < {n}; ++r) {nm}[r] = {tmp}[r];")
+
+    def op_if(self, op):
+        cond = self.name[op.operands[0].id]
+        names = []
+        for r in op.results:
+            t = ctype(r.type.dtype) + ("*" if r.type.ptr else "")
+            nm = self.fresh("f")
+            names.append(nm)
+            if self.tile(r):
+                self.emit(f"{t} {nm}[{self.lay[r.id].nregs}];")
+            else:
+                self.emit(f"{t} {nm};")
+        for i, reg in enumerate(op.regions):
+            self.push_scope(f"if ({cond}) {{" if i == 0 else "else {")
+            self.gen_block(reg)
+            y = reg.ops[-1]
+            for v, r, nm in zip(y.operands, op.results, names):
+                if self.tile(r):
+                    lay = self.lay[r.id]
+                    self.emit("#pragma unroll")
+                    self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = "
+                              f"{self.elem(v, lay, 'r')};")
+                else:
+                    self.emit(f"{nm} = {self.name[v.id]};")
+            self.pop_scope()
+        for r, nm in zip(op.results, names):
+            self.define(r, nm)
+
+    # ------------------------------------------------------------------ driver
+    def run(self) -> GeneratedKernel:
+        fn = self.fn
+        self.count_uses(fn.body)
+        args = []
+        params = []
+        for i, (a, nmh) in enumerate(zip(fn.args, fn.arg_names)):
+            self.vals[a.id] = a
+            t = a.type
+            if t.ptr:
+                self.kind[a.id] = "scalar"
+                cp = f"{ctype(t.dtype)}*"
+                args.append(KernelArg(nmh, "ptr", t.dtype, cp))
+                params.append(f"{cp} a{i}")
+                self.name[a.id] = f"a{i}"
+            else:
+                self.kind[a.id] = "scalar"
+                dt = t.dtype
+                cp = "int32_t" if dt.is_bool() else ctype(dt)
+                args.append(KernelArg(nmh, "scalar", dt, cp))
+                params.append(f"{cp} a{i}")
+                self.name[a.id] = f"a{i}" if not dt.is_bool() else f"((bool)a{i})"
+            self.def_level[a.id] = 0
+        self.assign_block(fn.body)
+        self.gen_block(fn.body)
+        kname = f"ek_{fn.name}"
+        out = ['#include "enceladus_cdna4.h"', ""]
+        out.append(f'extern "C" __global__ void __launch_bounds__({self.nt}) {kname}('
+                   + ", ".join(params) + ") {")
+        if self.lds:
+            lds = (self.lds + 15) // 16 * 16
+            out.append(f"  __shared__ __attribute__((aligned(16))) char ek_smem[{lds}];")
+        out.append("  const int ek_tid = threadIdx.x;")
+        out.append("  const int ek_lane = ek_tid & 63;")
+        out.append("  const int ek_warp = ek_tid >> 6;")
+        out.append("  (void)ek_lane; (void)ek_warp; (void)ek_tid;")
+        out.extend(self.prologue)
+
+        def flat(items):
+            for it in items:
+                if isinstance(it, list):
+                    yield from flat(it)
+                else:
+                    yield it
+        out.extend(flat(self.scopes[0].items))
+        out.append("}")
+        return GeneratedKernel(kname, "\n".join(out) + "\n", args, self.nw, self.lds, self.nt)
+
+
+def generate(fn: ir.Func, options: dict | None = None) -> GeneratedKernel:
+    return Emitter(fn, options).run()
+
+
+def pack_args(kargs: list[KernelArg], values: list) -> bytes:
+    """Packs runtime argument values into the kernarg layout (natural alignment)."""
+    buf = bytearray()
+    for ka, v in zip(kargs, values):
+        if ka.kind == "ptr":
+            fmt, size = "Q", 8
+            v = int(v)
+        else:
+            cp = ka.cparam
+            fmt, size = {"int32_t": ("i", 4), "int64_t": ("q", 8), "uint32_t": ("I", 4),
+                         "uint64_t": ("Q", 8), "float": ("f", 4), "int16_t": ("h", 2),
+                         "uint16_t": ("H", 2), "int8_t": ("b", 1), "uint8_t": ("B", 1)}[cp]
+            v = float(v) if fmt == "f" else int(v)
+        pad = (-len(buf)) % size
+        buf += b"\0" * pad
+        buf += struct.pack("<" + fmt, v)
+    buf += b"\0" * ((-len(buf)) % 8)
+    return bytes(buf)

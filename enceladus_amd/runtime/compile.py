@@ -1,0 +1,141 @@
+"""Specialization → code object, with an in-memory and on-disk cache.
+
+`compile_specialization` builds IR, runs the HIP emitter, compiles with hiprtc for gfx950
+and caches the code object under `$ENCELADUS_CACHE_DIR` (default
+`~/.cache/enceladus_amd`), keyed by the generated source, the compile options and the
+shim/header versions. Reference: src/enceladus/runtime/compile.py:38-164 and cache.py:26-144
+(disk cache of compiled kernels, corrupt entries recompiled).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import hashlib
+import logging
+import os
+import threading
+from pathlib import Path
+
+from enceladus_amd.compiler import codegen_hip, frontend, ir
+from enceladus_amd.runtime import hip
+
+log = logging.getLogger("enceladus")
+
+ARCH = os.environ.get("ENCELADUS_ARCH", "gfx950")
+BASE_OPTIONS = ["-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
+                "-packed-fp32-ops", "-fno-gpu-rdc", "-mcumode"]
+
+_mem_cache: dict[str, bytes] = {}
+_lock = threading.Lock()
+
+
+def cache_dir() -> Path:
+    d = os.environ.get("ENCELADUS_CACHE_DIR")
+    return Path(d) if d else Path.home() / ".cache" / "enceladus_amd"
+
+
+def _header_hash() -> str:
+    h = hashlib.sha256()
+    h.update((hip.INCLUDE_DIR / "enceladus_cdna4.h").read_bytes())
+    return h.hexdigest()[:16]
+
+
+_HDR = None
+
+
+def compile_options(extra=()) -> list[str]:
+    return [f"--offload-arch={ARCH}", *BASE_OPTIONS, f"-I{hip.INCLUDE_DIR}", *extra]
+
+
+def compile_code(src: str, name: str, extra=()) -> bytes:
+    """hiprtc-compiles `src` (cached by source hash)."""
+    global _HDR
+    if _HDR is None:
+        _HDR = _header_hash()
+    opts = compile_options(extra)
+    key = hashlib.sha256("\0".join([src, name, _HDR, *opts]).encode()).hexdigest()
+    with _lock:
+        hit = _mem_cache.get(key)
+    if hit is not None:
+        return hit
+    always = os.environ.get("ENCELADUS_ALWAYS_COMPILE") == "1"
+    path = cache_dir() / key[:2] / f"{key}.hsaco"
+    if not always and path.exists():
+        data = path.read_bytes()
+        if data[:4] == b"\x7fELF":
+            with _lock:
+                _mem_cache[key] = data
+            return data
+        log.debug("corrupt cache entry %s; recompiling", path)
+    data, text = hip.compile_source(src, f"{name}.hip", opts)
+    if text.strip():
+        log.debug("hiprtc log for %s:\n%s", name, text)
+    try:
+        path.parent.mkdir(parents=True, exist_ok=True)
+        tmp = path.with_suffix(f".tmp{os.getpid()}")
+        tmp.write_bytes(data)
+        os.replace(tmp, path)
+    except OSError:
+        pass
+    with _lock:
+        _mem_cache[key] = data
+    return data
+
+
+class CompiledKernel:
+    """A compiled specialization: source, IR text, code object and (lazily) its function."""
+
+    def __init__(self, gen: codegen_hip.GeneratedKernel, ir_text: str, code: bytes):
+        self.gen = gen
+        self.name = gen.name
+        self.hip = gen.source
+        self.msl = gen.source        # the reference's attribute name, kept for drop-in code
+        self.ir = ir_text
+        self.code = code
+        self.num_warps = gen.num_warps
+        self.threadgroup_memory_bytes = gen.lds_bytes
+        self.lds_bytes = gen.lds_bytes
+        self.args = gen.args
+        self._module = None
+        self._function = None
+        self._attrs = None
+
+    def function(self):
+        if self._function is None:
+            m = ctypes.c_void_p()
+            buf = ctypes.create_string_buffer(self.code, len(self.code))
+            hip.call("ek_module_load", buf, len(self.code), ctypes.byref(m))
+            f = ctypes.c_void_p()
+            hip.call("ek_module_function", m, self.name.encode(), ctypes.byref(f))
+            self._module, self._function = m, f
+        return self._function
+
+    @property
+    def attrs(self) -> dict:
+        if self._attrs is None:
+            a = hip.FunctionAttrs()
+            hip.call("ek_function_get_attrs", self.function(), ctypes.byref(a))
+            self._attrs = {"num_regs": a.num_regs, "shared_bytes": a.shared_bytes,
+                           "local_bytes": a.local_bytes, "max_threads": a.max_threads}
+        return self._attrs
+
+    def pack(self, values) -> bytes:
+        return codegen_hip.pack_args(self.args, values)
+
+    def launch_raw(self, grid, kernarg: bytes, stream: int = 0):
+        gx, gy, gz = (tuple(grid) + (1, 1, 1))[:3]
+        if gx == 0 or gy == 0 or gz == 0:
+            return
+        buf = ctypes.create_string_buffer(kernarg, len(kernarg))
+        hip.call("ek_launch", ctypes.c_void_p(stream or None), self.function(), gx, gy, gz,
+                 self.gen.block, 1, 1, 0, buf, len(kernarg))
+
+
+def compile_ir(fn: ir.Func, options: dict | None = None) -> CompiledKernel:
+    gen = codegen_hip.generate(fn, options)
+    code = compile_code(gen.source, gen.name)
+    return CompiledKernel(gen, ir.print_func(fn), code)
+
+
+def build_module(jfn, arg_types, arg_facts, constexprs, num_warps, options) -> ir.Func:
+    return frontend.build_ir(jfn.fn, arg_types, arg_facts, constexprs, num_warps, options)

@@ -1,0 +1,289 @@
+"""`@jit`, kernel specialization and the launch front door.
+
+`kernel[grid](*args, num_warps=4, dot_warps=None, **constexprs)` binds arguments, looks up
+the specialization (a dict hit when warm), compiles on a miss, packs the kernarg buffer
+and launches one workgroup of `num_warps * 64` threads per program. Reference:
+src/enceladus/runtime/jit.py (`JITFunction` :214-667, `run` :388, `_lookup` :449,
+`arg_type` :97, `arg_facts` :148, `jit` :1237, `cdiv`/`next_power_of_2` :64-71).
+
+`ENCELADUS_INTERPRET=1` (the reference's NumPy interpreter mode) is not part of this
+backend: the CPU interpreter is test infrastructure here, so requesting it raises.
+"""
+
+from __future__ import annotations
+
+import inspect
+import os
+from dataclasses import dataclass
+from typing import Any, Callable
+
+import numpy as np
+
+from enceladus_amd.compiler import ir
+from enceladus_amd.compiler.errors import CompilationError
+from enceladus_amd.language import core
+from enceladus_amd.runtime import compile as C
+from enceladus_amd.runtime import device as D
+from enceladus_amd.runtime import tensor as T
+
+
+def cdiv(x: int, y: int) -> int:
+    return (x + y - 1) // y
+
+
+def next_power_of_2(n: int) -> int:
+    n = int(n)
+    return 1 if n <= 1 else 1 << (n - 1).bit_length()
+
+
+def arg_type(value: Any) -> ir.TType:
+    if isinstance(value, (bool, np.bool_)):
+        return ir.TType((), core.int1)
+    if isinstance(value, np.uint64):
+        return ir.TType((), core.uint64)
+    if isinstance(value, (int, np.integer)):
+        v = int(value)
+        if -(1 << 31) <= v < (1 << 31):
+            return ir.TType((), core.int32)
+        if -(1 << 63) <= v < (1 << 63):
+            return ir.TType((), core.int64)
+        if 0 <= v < (1 << 64):
+            return ir.TType((), core.uint64)
+        raise TypeError(f"integer argument {v} doesn't fit in 64 bits")
+    if isinstance(value, (float, np.floating)):
+        return ir.TType((), core.float32)
+    if T.is_array_like(value):
+        return ir.TType((), T.elem_dtype(value), ptr=True)
+    raise TypeError(f"a {type(value).__name__} can't be a runtime kernel argument; annotate "
+                    "compile-time parameters as tl.constexpr")
+
+
+def _data_ptr(value: Any) -> int | None:
+    if isinstance(value, np.ndarray):
+        return value.__array_interface__["data"][0]
+    if isinstance(value, T.Tensor):
+        return value.ptr
+    p = getattr(value, "data_ptr", None)
+    return p() if callable(p) else None
+
+
+def arg_facts(value: Any) -> dict:
+    if isinstance(value, (bool, np.bool_, float, np.floating)):
+        return {}
+    if isinstance(value, (int, np.integer)):
+        v = int(value)
+        f = {}
+        if v % 16 == 0:
+            f["divisibility"] = 16
+        if v == 1:
+            f["equal_to_1"] = True
+        return f
+    if T.is_array_like(value):
+        p = _data_ptr(value)
+        if isinstance(value, np.ndarray):
+            return {"divisibility": 16}   # copied into a fresh 16-byte-aligned allocation
+        return {"divisibility": 16} if p is not None and p % 16 == 0 else {}
+    return {}
+
+
+@dataclass(frozen=True)
+class KernelParam:
+    name: str
+    index: int
+    is_constexpr: bool
+    default: Any
+    do_not_specialize: bool
+
+
+def _writes(fn: ir.Func) -> set[int]:
+    """Indices of pointer args the kernel may write through."""
+    roots = {}
+    out = set()
+    for i, a in enumerate(fn.args):
+        roots[a.id] = i
+    for op in ir.walk(fn.body):
+        if op.name in ("ptr_add", "broadcast", "splat", "expand_dims", "hint", "select",
+                       "trans", "make_desc"):
+            for o in op.operands[:1] if op.name != "select" else op.operands[1:]:
+                if o.id in roots and op.results:
+                    roots[op.result.id] = roots[o.id]
+        if op.name == "for":
+            body = op.regions[0]
+            for a, i in zip(body.args[1:], op.operands[3:]):
+                if i.id in roots:
+                    roots[a.id] = roots[i.id]
+            for r, i in zip(op.results, op.operands[3:]):
+                if i.id in roots:
+                    roots[r.id] = roots[i.id]
+        if op.name in ("store", "atomic_rmw", "atomic_cas", "desc_store"):
+            if op.operands[0].id in roots:
+                out.add(roots[op.operands[0].id])
+    return out
+
+
+class Launcher:
+    """A compiled kernel plus the per-specialization launch plan."""
+
+    def __init__(self, ck: C.CompiledKernel, runtime_names: list[str], writes: set[int],
+                 constexprs: dict):
+        self.ck = ck
+        self.runtime_names = runtime_names
+        self.writes = writes
+        self.constexprs = constexprs
+
+    def __call__(self, grid, values: list, stream: int | None = None):
+        bindings = []
+        packed = []
+        for i, v in enumerate(values):
+            if T.is_array_like(v):
+                b = T.bind_array(v)
+                b.writeback = i in self.writes
+                bindings.append(b)
+                packed.append(b.ptr)
+            else:
+                packed.append(v)
+        if stream is None:
+            stream = D.current_stream()
+        self.ck.launch_raw(grid, self.ck.pack(packed), stream)
+        if any(b.host is not None for b in bindings):
+            from enceladus_amd.runtime import hip
+            hip.call("ek_device_sync")
+            for b in bindings:
+                T.finish_binding(b)
+
+
+class JITFunction:
+    """A kernel or device function created by `@enceladus.jit`."""
+
+    _ek_jit = True
+
+    def __init__(self, fn: Callable, do_not_specialize=(), math_mode: str = "relaxed",
+                 interpret=None):
+        self.fn = fn
+        self.__name__ = fn.__name__
+        self.__doc__ = fn.__doc__
+        self.math_mode = math_mode
+        self.interpret = interpret
+        sig = inspect.signature(fn)
+        dns = set(do_not_specialize)
+        self.params = []
+        for i, p in enumerate(sig.parameters.values()):
+            self.params.append(KernelParam(
+                p.name, i, core.is_constexpr_annotation(p.annotation),
+                p.default if p.default is not inspect.Parameter.empty else inspect.Parameter.empty,
+                p.name in dns or i in dns))
+        self.arg_names = [p.name for p in self.params]
+        self._cache: dict[Any, Launcher] = {}
+
+    def __repr__(self):
+        return f"JITFunction({self.fn.__module__}:{self.__name__})"
+
+    def __call__(self, *args, **kwargs):
+        raise RuntimeError(f"`{self.__name__}` is an @enceladus.jit kernel: launch it as "
+                           f"{self.__name__}[grid](...), or call it from another kernel")
+
+    def __getitem__(self, grid):
+        return lambda *args, **kwargs: self.run(*args, grid=grid, **kwargs)
+
+    def _bind(self, args, kwargs):
+        vals = {}
+        if len(args) > len(self.params):
+            raise TypeError(f"{self.__name__} takes {len(self.params)} arguments, got {len(args)}")
+        for p, a in zip(self.params, args):
+            vals[p.name] = a
+        for k, v in kwargs.items():
+            if k not in self.arg_names:
+                raise TypeError(f"{self.__name__} got an unexpected argument `{k}`")
+            vals[k] = v
+        for p in self.params:
+            if p.name not in vals:
+                if p.default is inspect.Parameter.empty:
+                    raise TypeError(f"{self.__name__} is missing argument `{p.name}`")
+                vals[p.name] = p.default
+        return vals
+
+    def specialize(self, vals: dict):
+        types, facts, consts = {}, {}, {}
+        for p in self.params:
+            v = vals[p.name]
+            if p.is_constexpr:
+                consts[p.name] = core.unwrap(v)
+                continue
+            types[p.name] = arg_type(v)
+            f = arg_facts(v)
+            if p.do_not_specialize:
+                f = {}
+            facts[p.name] = f
+        return types, facts, consts
+
+    def _key(self, types, facts, consts, num_warps, dot_warps):
+        def ck(v):
+            if isinstance(v, core.dtype):
+                return ("dt", v.name)
+            if isinstance(v, (list, tuple)):
+                return tuple(ck(x) for x in v)
+            return (type(v).__name__, v)
+        return (tuple((k, str(t)) for k, t in types.items()),
+                tuple((k, tuple(sorted(f.items()))) for k, f in facts.items()),
+                tuple((k, ck(v)) for k, v in consts.items()), num_warps,
+                tuple(dot_warps) if dot_warps else None)
+
+    def _compile_for(self, types, facts, consts, num_warps, dot_warps) -> Launcher:
+        options = {"dot_warps": tuple(dot_warps) if dot_warps else None}
+        fn_ir = C.build_module(self, types, facts, consts, num_warps, options)
+        ck = C.compile_ir(fn_ir, options)
+        runtime_names = list(types.keys())
+        return Launcher(ck, runtime_names, _writes(fn_ir), consts)
+
+    def _lookup(self, vals, num_warps, dot_warps) -> Launcher:
+        types, facts, consts = self.specialize(vals)
+        key = self._key(types, facts, consts, num_warps, dot_warps)
+        lc = self._cache.get(key)
+        if lc is None:
+            lc = self._compile_for(types, facts, consts, num_warps, dot_warps)
+            self._cache[key] = lc
+        return lc
+
+    def run(self, *args, grid, num_warps: int = 4, num_stages=None, dot_warps=None,
+            dot_backend: str = "auto", stream=None, **kwargs):
+        if self.interpret or os.environ.get("ENCELADUS_INTERPRET") == "1":
+            raise RuntimeError("ENCELADUS_INTERPRET=1 selects the CPU interpreter, which this "
+                               "MI355X backend ships only as test infrastructure (oracle/); "
+                               "unset it to run on the GPU")
+        if num_warps not in (1, 2, 4, 8, 16):
+            raise ValueError(f"num_warps must be 1, 2, 4, 8 or 16 (wave64), got {num_warps}")
+        vals = self._bind(args, kwargs)
+        lc = self._lookup(vals, num_warps, dot_warps)
+        if callable(grid):
+            grid = grid(dict(vals))
+        grid = tuple(int(g) for g in (grid if isinstance(grid, (tuple, list)) else (grid,)))
+        if not 1 <= len(grid) <= 3:
+            raise ValueError(f"grid must have 1 to 3 dimensions, got {grid}")
+        if grid[0] >= 1 << 31 or any(g > 65535 for g in grid[1:]) or any(g < 0 for g in grid):
+            raise ValueError(f"grid {grid} exceeds the HIP limits (x < 2^31, y, z <= 65535)")
+        values = [vals[n] for n in lc.runtime_names]
+        lc(grid, values, stream)
+        return lc.ck
+
+    def warmup(self, *args, num_warps: int = 4, dot_warps=None, grid=None, **kwargs):
+        vals = self._bind(args, kwargs)
+        return self._lookup(vals, num_warps, dot_warps).ck
+
+    def ir_for(self, *args, num_warps: int = 4, dot_warps=None, **kwargs) -> ir.Func:
+        vals = self._bind(args, kwargs)
+        types, facts, consts = self.specialize(vals)
+        return C.build_module(self, types, facts, consts, num_warps,
+                              {"dot_warps": tuple(dot_warps) if dot_warps else None})
+
+    def explain(self, *args, **kwargs) -> str:
+        ck = self.warmup(*args, **kwargs)
+        return (f"kernel {ck.name}: num_warps={ck.num_warps} lds={ck.lds_bytes}B\n"
+                f"--- IR ---\n{ck.ir}\n--- HIP ---\n{ck.hip}")
+
+
+def jit(fn=None, *, interpret=None, do_not_specialize=(), math_mode: str = "relaxed"):
+    def deco(f):
+        return JITFunction(f, do_not_specialize, math_mode, interpret)
+    if fn is not None:
+        return deco(fn)
+    return deco

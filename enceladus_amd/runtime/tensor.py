@@ -1,0 +1,235 @@
+"""Device tensors in HBM and array interop (NumPy, torch-ROCm, and our own `Tensor`).
+
+Reference: `Tensor` and the array adapters (src/enceladus/runtime/tensor.py:65-363,
+runtime/interop.py:38-62, 161, 323-420, 577). On MI355X a NumPy argument is copied into
+HBM for the launch and copied back afterwards if the kernel writes it; a torch tensor on
+the GPU or a `Tensor` is passed by device pointer with no copy.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import sys
+from typing import Any
+
+import numpy as np
+
+from enceladus_amd.language import core
+from enceladus_amd.runtime import hip
+
+
+class Tensor:
+    """A contiguous device array owned by this runtime."""
+
+    def __init__(self, shape, dtype: core.dtype):
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = dtype
+        n = 1
+        for s in self.shape:
+            n *= s
+        self.numel = n
+        self.nbytes = n * dtype.itemsize
+        p = ctypes.c_void_p()
+        hip.call("ek_malloc", ctypes.byref(p), max(self.nbytes, 16))
+        self.ptr = p.value or 0
+        self._owner = True
+        s = 1
+        st = []
+        for d in reversed(self.shape):
+            st.append(s)
+            s *= d
+        self.strides = tuple(reversed(st))
+
+    def data_ptr(self) -> int:
+        return self.ptr
+
+    def __del__(self):
+        if getattr(self, "_owner", False) and self.ptr:
+            try:
+                hip.call("ek_free", ctypes.c_void_p(self.ptr))
+            except Exception:  # noqa: BLE001
+                pass
+            self.ptr = 0
+
+    def numpy(self) -> np.ndarray:
+        out = np.empty(self.shape, self.dtype.to_numpy())
+        if self.nbytes:
+            hip.call("ek_memcpy_d2h", out.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(self.ptr),
+                     self.nbytes, None)
+        return out
+
+    def copy_from_numpy(self, a: np.ndarray) -> "Tensor":
+        a = np.ascontiguousarray(a)
+        if a.nbytes != self.nbytes:
+            raise ValueError("size mismatch")
+        if self.nbytes:
+            hip.call("ek_memcpy_h2d", ctypes.c_void_p(self.ptr), a.ctypes.data_as(ctypes.c_void_p),
+                     self.nbytes, None)
+        return self
+
+    def __repr__(self):
+        return f"Tensor(shape={self.shape}, dtype={self.dtype})"
+
+
+def empty(shape, dtype=core.float32) -> Tensor:
+    if isinstance(shape, int):
+        shape = (shape,)
+    return Tensor(shape, _as_dtype(dtype))
+
+
+def zeros(shape, dtype=core.float32) -> Tensor:
+    t = empty(shape, dtype)
+    if t.nbytes:
+        hip.call("ek_memset", ctypes.c_void_p(t.ptr), 0, t.nbytes, None)
+        hip.call("ek_device_sync")
+    return t
+
+
+def from_numpy(a: np.ndarray, dtype=None) -> Tensor:
+    dt = _as_dtype(dtype) if dtype is not None else core.dtype_from_numpy(a.dtype)
+    t = Tensor(a.shape, dt)
+    return t.copy_from_numpy(a)
+
+
+def randn(*shape, dtype=core.float32, seed: int = 0) -> Tensor:
+    rng = np.random.default_rng(seed)
+    return from_numpy(rng.standard_normal(shape, dtype=np.float32).astype(
+        _as_dtype(dtype).to_numpy()), dtype)
+
+
+def _as_dtype(dt) -> core.dtype:
+    if isinstance(dt, core.dtype):
+        return dt
+    if isinstance(dt, str):
+        return core.dtype_from_name(dt)
+    return core.dtype_from_numpy(dt)
+
+
+# ---------------------------------------------------------------------------------------
+# Interop helpers used by examples (reference: runtime/interop.py:323-420)
+# ---------------------------------------------------------------------------------------
+
+def _is_torch(x: Any) -> bool:
+    t = sys.modules.get("torch")
+    return t is not None and isinstance(x, t.Tensor)
+
+
+def element_dtype(x: Any) -> np.dtype:
+    if isinstance(x, Tensor):
+        return x.dtype.to_numpy()
+    if _is_torch(x):
+        dt = core.dtype_from_torch(x.dtype)
+        return dt.to_numpy()
+    return np.asarray(x).dtype
+
+
+def elem_dtype(x: Any) -> core.dtype:
+    if isinstance(x, Tensor):
+        return x.dtype
+    if _is_torch(x):
+        return core.dtype_from_torch(x.dtype)
+    return core.dtype_from_numpy(np.asarray(x).dtype)
+
+
+def element_strides(x: Any) -> tuple[int, ...]:
+    if isinstance(x, Tensor):
+        return x.strides
+    if _is_torch(x):
+        return tuple(x.stride())
+    a = np.asarray(x)
+    return tuple(s // a.itemsize for s in a.strides)
+
+
+def new_empty(x: Any, shape=None, dtype=None):
+    shape = tuple(x.shape) if shape is None else tuple(shape)
+    if _is_torch(x):
+        import torch
+        tdt = x.dtype if dtype is None else _torch_dtype(dtype)
+        return torch.empty(shape, dtype=tdt, device=x.device)
+    if isinstance(x, Tensor):
+        return empty(shape, x.dtype if dtype is None else _as_dtype(dtype))
+    npdt = np.asarray(x).dtype if dtype is None else np.dtype(dtype) if not isinstance(
+        dtype, core.dtype) else dtype.to_numpy()
+    return np.empty(shape, npdt)
+
+
+def new_zeros(x: Any, shape=None, dtype=None):
+    shape = tuple(x.shape) if shape is None else tuple(shape)
+    if _is_torch(x):
+        import torch
+        tdt = x.dtype if dtype is None else _torch_dtype(dtype)
+        return torch.zeros(shape, dtype=tdt, device=x.device)
+    if isinstance(x, Tensor):
+        return zeros(shape, x.dtype if dtype is None else _as_dtype(dtype))
+    npdt = np.asarray(x).dtype if dtype is None else np.dtype(dtype) if not isinstance(
+        dtype, core.dtype) else dtype.to_numpy()
+    return np.zeros(shape, npdt)
+
+
+def _torch_dtype(dt):
+    import torch
+    if isinstance(dt, core.dtype):
+        name = dt.long_name
+    else:
+        name = np.dtype(dt).name
+    return getattr(torch, {"int1": "bool"}.get(name, name))
+
+
+def is_array_like(x: Any) -> bool:
+    return isinstance(x, (np.ndarray, Tensor)) or _is_torch(x)
+
+
+class Binding:
+    """One array argument bound for a launch: its device pointer, plus a copy-back."""
+
+    __slots__ = ("ptr", "host", "dev", "writeback", "keep")
+
+    def __init__(self, ptr, host=None, dev=None, keep=None):
+        self.ptr = ptr
+        self.host = host
+        self.dev = dev
+        self.writeback = False
+        self.keep = keep
+
+
+def bind_array(x: Any) -> Binding:
+    if isinstance(x, Tensor):
+        return Binding(x.ptr, keep=x)
+    if _is_torch(x):
+        if x.device.type == "cuda":
+            return Binding(int(x.data_ptr()), keep=x)
+        a = x.detach().numpy()
+        dev = Tensor((a.nbytes,), core.uint8)
+        if a.nbytes:
+            hip.call("ek_memcpy_h2d", ctypes.c_void_p(dev.ptr), a.ctypes.data_as(ctypes.c_void_p),
+                     a.nbytes, None)
+        return Binding(dev.ptr, host=a, dev=dev)
+    a = x if isinstance(x, np.ndarray) else np.asarray(x)
+    if not (a.flags.c_contiguous or a.flags.f_contiguous):
+        base = a
+        while base.base is not None and isinstance(base.base, np.ndarray):
+            base = base.base
+    n = _span_bytes(a)
+    dev = Tensor((max(n, 1),), core.uint8)
+    if n:
+        start = a.__array_interface__["data"][0]
+        hip.call("ek_memcpy_h2d", ctypes.c_void_p(dev.ptr), ctypes.c_void_p(start), n, None)
+    return Binding(dev.ptr, host=a, dev=dev)
+
+
+def _span_bytes(a: np.ndarray) -> int:
+    if a.size == 0:
+        return 0
+    if any(s < 0 for s in a.strides):
+        raise ValueError("arrays with negative strides can't be kernel arguments")
+    return a.itemsize * (1 + sum((n - 1) * (s // a.itemsize) for n, s in zip(a.shape, a.strides)))
+
+
+def finish_binding(b: Binding) -> None:
+    if b.host is None or not b.writeback:
+        return
+    a = b.host
+    n = _span_bytes(a)
+    if n:
+        start = a.__array_interface__["data"][0]
+        hip.call("ek_memcpy_d2h", ctypes.c_void_p(start), ctypes.c_void_p(b.dev.ptr), n, None)

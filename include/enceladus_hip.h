@@ -1,0 +1,111 @@
+/*
+ * enceladus_hip.h — the C ABI of the MI355X runtime shim (libenceladus_hip.so).
+ *
+ * It replaces the reference's Objective-C++ Metal runtime ABI (`fr_*`, reference
+ * src/enceladus/_C/enceladus_rt.h:13-166). Conventions kept from it:
+ *   - opaque handles, each with an explicit release;
+ *   - 0 on success, non-zero on failure, with the error text written into a
+ *     caller-provided buffer (`err`, `errlen`; the reference uses FR_ERR_LEN=65536);
+ *   - plain pointers and sizes only, so any FFI (ctypes here) can bind it.
+ * All functions are thread-safe: hiprtc programs are per call, and HIP streams are
+ * internally synchronized.
+ */
+#ifndef ENCELADUS_HIP_H
+#define ENCELADUS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EK_ERR_LEN 65536
+
+/* Device query. Replaces fr_device_* (reference _C/enceladus_rt.mm:39-79). */
+typedef struct ek_device_info {
+  char name[256];
+  char arch[64];            /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+  int32_t compute_units;
+  int32_t warp_size;        /* 64 on CDNA */
+  int32_t max_threads_per_block;
+  int64_t lds_per_block;    /* bytes */
+  int64_t total_mem;        /* bytes */
+  int32_t clock_khz;
+  int32_t mem_clock_khz;
+  int32_t mem_bus_width;
+  int32_t l2_bytes;
+} ek_device_info;
+
+int ek_device_count(int* count, char* err, size_t errlen);
+int ek_device_get_info(int device, ek_device_info* out, char* err, size_t errlen);
+int ek_set_device(int device, char* err, size_t errlen);
+
+/* Runtime compile: HIP C++ source -> gfx950 code object via hiprtc.
+ * Replaces fr_library_new (reference _C/enceladus_rt.mm:208-230).
+ * On success *code is a malloc'd buffer of *code_size bytes (free with ek_buffer_free);
+ * the hiprtc log (warnings or errors) is written into `log`. */
+int ek_compile(const char* source, const char* name, const char* const* options,
+               int num_options, void** code, size_t* code_size, char* log, size_t loglen);
+void ek_buffer_free(void* p);
+
+/* Module and kernel handles. Replaces fr_pipeline_new + reflection
+ * (reference _C/enceladus_rt.mm:251-313). */
+int ek_module_load(const void* code, size_t code_size, void** module, char* err, size_t errlen);
+int ek_module_unload(void* module, char* err, size_t errlen);
+int ek_module_function(void* module, const char* name, void** function, char* err,
+                       size_t errlen);
+typedef struct ek_function_attrs {
+  int32_t num_regs;
+  int32_t shared_bytes;      /* static LDS */
+  int32_t local_bytes;       /* scratch (register spills) per thread */
+  int32_t max_threads;
+} ek_function_attrs;
+int ek_function_get_attrs(void* function, ek_function_attrs* out, char* err, size_t errlen);
+
+/* Launch with a packed kernarg buffer (natural alignment, as the AMDGPU ABI lays out
+ * kernel parameters). Replaces fr_stream_dispatch/encode (reference
+ * _C/enceladus_rt.mm:394-427). `stream` may be NULL for the null stream. */
+int ek_launch(void* stream, void* function, uint32_t gx, uint32_t gy, uint32_t gz,
+              uint32_t bx, uint32_t by, uint32_t bz, uint32_t dyn_lds, void* kernarg,
+              size_t kernarg_size, char* err, size_t errlen);
+
+/* Streams. Replaces fr_stream_new/fr_stream_sync (reference _C/enceladus_rt.mm:357-577). */
+int ek_stream_new(void** stream, char* err, size_t errlen);
+int ek_stream_free(void* stream, char* err, size_t errlen);
+int ek_stream_sync(void* stream, char* err, size_t errlen);
+int ek_device_sync(char* err, size_t errlen);
+
+/* Device memory. Replaces shared MTLBuffers (reference _C/enceladus_rt.mm:317-352). */
+int ek_malloc(void** ptr, size_t bytes, char* err, size_t errlen);
+int ek_free(void* ptr, char* err, size_t errlen);
+int ek_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream, char* err,
+                  size_t errlen);
+int ek_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream, char* err,
+                  size_t errlen);
+int ek_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream, char* err,
+                  size_t errlen);
+int ek_memset(void* dst, int value, size_t bytes, void* stream, char* err, size_t errlen);
+
+/* GPU timing with events on `stream`. Replaces fr_stream_timed_run /
+ * fr_stream_flush_timed (reference _C/enceladus_rt.mm:605, 626). */
+int ek_event_new(void** event, char* err, size_t errlen);
+int ek_event_free(void* event, char* err, size_t errlen);
+int ek_event_record(void* event, void* stream, char* err, size_t errlen);
+int ek_event_elapsed_ms(void* start, void* stop, float* ms, char* err, size_t errlen);
+
+/* Launches `function` `reps` times back to back between two events and returns the
+ * average milliseconds per launch. */
+int ek_timed_launch(void* stream, void* function, uint32_t gx, uint32_t gy, uint32_t gz,
+                    uint32_t bx, uint32_t by, uint32_t bz, uint32_t dyn_lds, void* kernarg,
+                    size_t kernarg_size, int reps, float* ms_per_launch, char* err,
+                    size_t errlen);
+
+/* Version string of the shim and of the HIP runtime it runs on. */
+const char* ek_version(void);
+int ek_runtime_version(int* version);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

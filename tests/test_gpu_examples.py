@@ -1,0 +1,159 @@
+"""GPU parity: each workload kernel on the HIP path against the CPU oracle and the
+closed forms, on identical seeded inputs (reference test strategy: tests/conftest.py:102-145,
+test_interpreter.py:37-112, test_attention.py:20-49, test_atomics_scans.py:200-227).
+
+Integer kernels (cumsum, histogram) must match bit for bit; vector add is bit-exact (IEEE
+add on both sides); float kernels use the tolerances stated in each test.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import interpreter as O
+from oracle import reference_np as R
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+@pytest.mark.parametrize("n", [1, 1000, 65539, 100_000])
+def test_vector_add(n):
+    from examples.vector_add import add, add_kernel
+    _say(f"vector_add n={n}")
+    x = np.random.default_rng(0).standard_normal(n, dtype=np.float32)
+    y = np.ones_like(x)
+    got = add(x, y)
+    want = np.empty_like(x)
+    O.run_grid(add_kernel, ((n + 1023) // 1024,), x, y, want, n, BLOCK=1024)
+    assert np.array_equal(got, want)
+    assert np.array_equal(got, x + y)
+
+
+@pytest.mark.parametrize("shape", [(64, 1000), (16, 8192), (3, 33)])
+def test_softmax(shape):
+    from examples.softmax import softmax, softmax_kernel
+    _say(f"softmax {shape}")
+    x = np.random.default_rng(0).standard_normal(shape, dtype=np.float32)
+    got = softmax(x)
+    want = np.empty_like(x)
+    O.run_grid(softmax_kernel, (shape[0],), want, x, shape[1], shape[1], shape[1],
+               BLOCK=1 << (shape[1] - 1).bit_length())
+    # outputs are ~1/n: relative 1e-5 with a small absolute floor
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-8)
+    np.testing.assert_allclose(got, R.softmax(x), rtol=1e-5, atol=1e-8)
+
+
+@pytest.mark.parametrize("shape", [(32, 1000), (8, 8192)])
+def test_rmsnorm(shape):
+    from examples.rmsnorm import rmsnorm
+    _say(f"rmsnorm {shape}")
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal(shape, dtype=np.float32)
+    w = np.random.default_rng(1).uniform(0.5, 1.5, shape[1]).astype(np.float32)
+    got = rmsnorm(x, w)
+    np.testing.assert_allclose(got, R.rmsnorm(x, w), rtol=1e-5, atol=1e-5)
+
+
+def test_layernorm():
+    from examples.layernorm import layernorm
+    _say("layernorm 32x1000 block 256")
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((32, 1000), dtype=np.float32)
+    w = rng.standard_normal(1000, dtype=np.float32)
+    b = rng.standard_normal(1000, dtype=np.float32)
+    y, mean, rstd = layernorm(x, w, b, block=256)
+    ry, rm, rr = R.layernorm(x, w, b)
+    np.testing.assert_allclose(y, ry, rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(mean, rm, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(rstd, rr, rtol=1e-5, atol=1e-5)
+
+
+def test_fused_gelu():
+    from examples.fused_gelu import fused_gelu
+    _say("fused_gelu 64x300")
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((64, 300), dtype=np.float32)
+    bias = rng.standard_normal(300, dtype=np.float32)
+    got = fused_gelu(x, bias, 0.5)
+    np.testing.assert_allclose(got, R.fused_gelu(x, bias, 0.5), rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("shape,reverse", [((8, 4096), False), ((300, 1000), False),
+                                           ((37, 50), True), ((5, 4096), True),
+                                           ((64, 256), False)])
+def test_cumsum_int32(shape, reverse):
+    from examples.cumsum import cumsum, cumsum_kernel
+    _say(f"cumsum {shape} reverse={reverse}")
+    x = np.random.default_rng(0).integers(-100, 100, shape, dtype=np.int32)
+    got = cumsum(x, reverse)
+    m, n = shape
+    bn = 1 << (n - 1).bit_length()
+    bm = max(1, min(16, 4096 // bn))
+    want = np.empty_like(x)
+    O.run_grid(cumsum_kernel, ((m + bm - 1) // bm,), want, x, m, n, n, n, REVERSE=reverse,
+               BLOCK_M=bm, BLOCK_N=bn)
+    assert np.array_equal(got, want)
+    assert np.array_equal(got, R.cumsum(x, reverse))
+
+
+@pytest.mark.parametrize("n,bins", [(1 << 20, 1024), (100_003, 64), (5000, 4096)])
+def test_histogram(n, bins):
+    from examples.histogram import histogram
+    _say(f"histogram n={n} bins={bins}")
+    x = np.random.default_rng(0).integers(0, bins, n, dtype=np.int32)
+    got = histogram(x, bins, 0.0, float(bins))
+    assert np.array_equal(got, R.histogram(x, bins, 0.0, float(bins)))
+    assert int(got.sum()) == n
+
+
+def _half(shape, seed, scale=1 / 64):
+    return (np.random.default_rng(seed).standard_normal(shape, dtype=np.float32) * scale
+            ).astype(np.float16)
+
+
+@pytest.mark.parametrize("m,n,k,bm,bn,bk,nw", [(128, 128, 128, 128, 128, 64, 4),
+                                                (256, 256, 256, 128, 128, 64, 4),
+                                                (100, 90, 70, 64, 64, 32, 4),
+                                                (64, 64, 64, 64, 64, 32, 4),
+                                                (256, 128, 512, 64, 128, 64, 4)])
+def test_matmul_desc(m, n, k, bm, bn, bk, nw):
+    from examples.matmul import matmul_desc
+    _say(f"matmul_desc {m}x{n}x{k} tile {bm}x{bn}x{bk}")
+    a, b = _half((m, k), 0, 1 / 8), _half((k, n), 1, 1 / 8)
+    got = matmul_desc(a, b, bm=bm, bn=bn, bk=bk, num_warps=nw).astype(np.float32)
+    want = R.matmul(a, b).astype(np.float32)
+    np.testing.assert_allclose(got, want, rtol=2e-3, atol=1e-3)
+
+
+def test_matmul_pointer_tiles():
+    from examples.matmul import matmul
+    _say("matmul pointer tiles 100x90x70")
+    a, b = _half((100, 70), 0, 1 / 8), _half((70, 90), 1, 1 / 8)
+    got = matmul(a, b).astype(np.float32)
+    np.testing.assert_allclose(got, R.matmul(a, b).astype(np.float32), rtol=2e-3, atol=1e-3)
+
+
+def test_matmul_bias_gelu():
+    from examples.matmul_fused import matmul_bias_gelu
+    _say("matmul_bias_gelu 256x256x128")
+    a, b = _half((256, 128), 0, 1 / 8), _half((128, 256), 1, 1 / 8)
+    bias = np.random.default_rng(2).standard_normal(256, dtype=np.float32).astype(np.float16)
+    got = matmul_bias_gelu(a, b, bias).astype(np.float32)
+    want = R.matmul_bias_gelu(a, b, bias).astype(np.float32)
+    np.testing.assert_allclose(got, want, rtol=2e-3, atol=2e-3)
+
+
+@pytest.mark.parametrize("causal,n,d,bm,bn", [(True, 256, 128, 128, 64), (False, 256, 128, 128, 64),
+                                              (True, 200, 64, 64, 32), (False, 128, 32, 64, 32)])
+def test_flash_attention_fp16(causal, n, d, bm, bn):
+    from examples.flash_attention import attention
+    _say(f"flash attention fp16 causal={causal} n={n} d={d}")
+    rng = np.random.default_rng(0)
+    q, k, v = (rng.standard_normal((1, 2, n, d), dtype=np.float32).astype(np.float16)
+               for _ in range(3))
+    got = attention(q, k, v, causal, block_m=bm, block_n=bn).astype(np.float64)
+    want = R.attention(q, k, v, causal)
+    np.testing.assert_allclose(got, want, rtol=2e-3, atol=2e-3)
