@@ -448,6 +448,9 @@ def to_tile(x, dt: dtype | None = None) -> OTile:
     x = _uw(x)
     if isinstance(x, OTile):
         return _cast(x, dt) if dt is not None else x
+    if isinstance(x, np.ndarray) and x.ndim > 0:
+        t = OTile(x, as_dtype(x.dtype))
+        return _cast(t, dt) if dt is not None else t
     if isinstance(x, np.generic):
         x = x.item()
     dt = dt or literal_dtype(x)

@@ -1,0 +1,95 @@
+"""Frontend and JIT behaviour on the CPU: IR shape, compile-time folding, error messages,
+specialization keys, and the interpreter-mode boundary."""
+
+import numpy as np
+import pytest
+
+import enceladus
+import enceladus.language as tl
+from enceladus_amd.compiler import ir
+from enceladus_amd.compiler.errors import CompilationError
+
+
+@enceladus.jit
+def _loop_kernel(x_ptr, n, BLOCK: tl.constexpr):
+    acc = tl.zeros([BLOCK], dtype=tl.float32)
+    for i in range(0, n, BLOCK):
+        acc += tl.load(x_ptr + i + tl.arange(0, BLOCK), mask=i + tl.arange(0, BLOCK) < n)
+    tl.store(x_ptr + tl.arange(0, BLOCK), acc)
+
+
+def test_runtime_loop_carries_accumulator():
+    f = _loop_kernel.ir_for(np.zeros(4, np.float32), 100, BLOCK=64)
+    fors = [op for op in ir.walk(f.body) if op.name == "for"]
+    assert len(fors) == 1 and len(fors[0].results) == 1
+    assert fors[0].results[0].type == ir.TType((64,), enceladus.language.float32)
+
+
+@enceladus.jit
+def _bad_shape(x_ptr, n):
+    tl.store(x_ptr + tl.arange(0, 100), 1.0)
+
+
+def test_non_power_of_two_arange_is_rejected():
+    with pytest.raises(CompilationError, match="power-of-two"):
+        _bad_shape.ir_for(np.zeros(4, np.float32), 3)
+
+
+@enceladus.jit
+def _while_kernel(x_ptr, n):
+    while n > 0:
+        n = n - 1
+
+
+def test_while_is_rejected_with_location():
+    with pytest.raises(CompilationError) as e:
+        _while_kernel.ir_for(np.zeros(4, np.float32), 3)
+    assert "while" in str(e.value) and "test_frontend.py" in str(e.value)
+
+
+@enceladus.jit
+def _dot_bad(a_ptr, BLOCK: tl.constexpr):
+    a = tl.load(a_ptr + tl.arange(0, BLOCK)[:, None] * BLOCK + tl.arange(0, BLOCK)[None, :])
+    b = tl.load(a_ptr + tl.arange(0, 2 * BLOCK)[:, None] + tl.arange(0, BLOCK)[None, :])
+    tl.dot(a, b)
+
+
+def test_dot_shape_mismatch():
+    with pytest.raises(CompilationError, match="inner dimensions"):
+        _dot_bad.ir_for(np.zeros(4, np.float16), BLOCK=16)
+
+
+def test_constexpr_branches_fold():
+    @enceladus.jit
+    def k(x_ptr, FLAG: tl.constexpr):
+        if FLAG:
+            tl.store(x_ptr, 1.0)
+        else:
+            tl.store(x_ptr, 2.0)
+    f = k.ir_for(np.zeros(1, np.float32), FLAG=True)
+    assert not any(op.name == "if" for op in ir.walk(f.body))
+
+
+def test_specialization_facts():
+    from enceladus_amd.runtime.jit import arg_facts, arg_type
+    assert arg_facts(32) == {"divisibility": 16}
+    assert arg_facts(1) == {"equal_to_1": True}
+    assert arg_type(1 << 40).dtype is tl.int64
+    assert arg_type(2.5).dtype is tl.float32
+
+
+def test_interpreter_mode_is_not_a_product_fallback(monkeypatch):
+    monkeypatch.setenv("ENCELADUS_INTERPRET", "1")
+    from examples.vector_add import add
+    with pytest.raises(RuntimeError, match="oracle"):
+        add(np.zeros(4, np.float32), np.zeros(4, np.float32))
+
+
+def test_calling_kernel_directly_raises():
+    with pytest.raises(RuntimeError, match=r"\[grid\]"):
+        _loop_kernel(1, 2)
+
+
+def test_tl_names_outside_kernels_raise():
+    with pytest.raises(RuntimeError):
+        tl.program_id(0)
