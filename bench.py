@@ -82,6 +82,11 @@ def make_launch(jfn, grid, args, num_warps=4, dot_warps=None, **constexprs):
     return launch
 
 
+# (BM, BN, BK, num_warps) swept for the matmul rows: the autotuner's MI355X candidates
+MATMUL_CONFIGS = [(256, 256, 64, 4), (256, 256, 32, 4), (256, 128, 64, 4), (128, 256, 64, 4),
+                  (128, 128, 64, 4), (256, 256, 64, 8)]
+
+
 def sets_for(bytes_per_set):
     return max(2, math.ceil(600e6 / bytes_per_set))
 
@@ -143,16 +148,22 @@ def w_matmul(torch, timer, steps, warmup, fused=False):
     b = (torch.randn(K, N, generator=g) / 64).half().cuda()
     bias = torch.randn(N, generator=g).half().cuda()
     c = torch.empty(M, N, dtype=torch.float16, device="cuda")
-    cfg = dict(BM=128, BN=128, BK=64)
-    grid = (N // 128, M // 128)
-    if fused:
-        l = make_launch(matmul_bias_gelu_kernel, grid, (a, b, bias, c, M, N, K, K, N, N), **cfg)
-    else:
-        l = make_launch(matmul_desc_kernel, grid, (a, b, c, M, N, K, K, N, N), **cfg)
-    ms = timer.run([l], max(5, steps // 2), max(2, warmup // 2))
+    best = None
+    for bm, bn, bk, nw in MATMUL_CONFIGS:
+        cfg = dict(BM=bm, BN=bn, BK=bk, num_warps=nw)
+        grid = (N // bn, M // bm)
+        if fused:
+            l = make_launch(matmul_bias_gelu_kernel, grid, (a, b, bias, c, M, N, K, K, N, N), **cfg)
+        else:
+            l = make_launch(matmul_desc_kernel, grid, (a, b, c, M, N, K, K, N, N), **cfg)
+        ms = timer.run([l], max(5, steps // 2), max(2, warmup // 2))
+        log(f"    BM={bm} BN={bn} BK={bk} warps={nw}: {ms * 1e3:.1f} us")
+        if best is None or ms < best[0]:
+            best = (ms, l, cfg)
+    ms, l, cfg = best
     flop = 2 * M * N * K
     return {"name": "matmul_gelu" if fused else "matmul", "config": "fp16 4096^3 fp32 acc"
-            + (" + bias + GELU" if fused else ""), "ms": ms, "flop": flop,
+            + (" + bias + GELU" if fused else "") + f" {cfg}", "ms": ms, "flop": flop,
             "tflops": flop / ms / 1e9, "bound": "mfma", "kernel": l.ck.name}
 
 

@@ -761,7 +761,7 @@ class Emitter:
     def op_program_id(self, op):
         nm = self.fresh("pid")
         ax = "xyz"[op.attrs["axis"]]
-        src = f"ek_pid_{ax}" if self.opt.get("_coarsen") else f"(int32_t)blockIdx.{ax}"
+        src = f"ek_pid_{ax}" if self.remap_pids else f"(int32_t)blockIdx.{ax}"
         self.emit(f"const int32_t {nm} = {src};")
         self.define(op.result, nm)
 
@@ -1329,8 +1329,119 @@ class Emitter:
             nm = out
         self.define(res, nm)
 
+    # -- dot loops on the GEMM template ---------------------------------------------------
+    def _gemm_match(self, op):
+        """Matches `for k in range(lo, hi, BK): acc = dot(dA.load([m0, k]), dB.load([k, n0]),
+        acc)` with loop-invariant m0/n0, 16-bit operands and aligned row-major tiles.
+        Returns a dict for the template, or None to use the generic lowering."""
+        body = op.regions[0]
+        iv, carried = body.args[0], body.args[1:]
+        if len(carried) != 1:
+            return None
+        acc = carried[0]
+        ops = body.ops[:-1]
+        y = body.ops[-1]
+        dots = [o for o in ops if o.name == "dot"]
+        loads = [o for o in ops if o.name == "desc_load"]
+        if len(dots) != 1 or len(loads) != 2:
+            return None
+        dot = dots[0]
+        a, b, c = dot.operands
+        if c.id != acc.id or y.operands[0].id != dot.result.id:
+            return None
+        if len(self.uses.get(acc.id, [])) != 1:
+            return None
+        la = a.op if a.op in loads else None
+        lb = b.op if b.op in loads else None
+        if la is None or lb is None:
+            return None
+        if len(self.uses.get(a.id, [])) != 1 or len(self.uses.get(b.id, [])) != 1:
+            return None
+        scalar_ops = []
+        for o in ops:
+            if o in (dot, la, lb):
+                continue
+            if o.regions or not o.results or self.tile(o.result) or \
+                    isinstance(o.result.type, ir.DescType) or o.name in (
+                        "load", "atomic_rmw", "atomic_cas", "store", "desc_store"):
+                return None
+            scalar_ops.append(o)
+        dep = {iv.id}
+        for o in scalar_ops:
+            if any(x.id in dep for x in o.operands):
+                dep.add(o.result.id)
+        da, db = la.operands[0], lb.operands[0]
+        if da.id not in self.desc or db.id not in self.desc:
+            return None
+        if la.operands[2].id != iv.id or lb.operands[1].id != iv.id:
+            return None
+        if la.operands[1].id in dep or lb.operands[2].id in dep:
+            return None
+        dt = a.type.dtype
+        if dt not in (core.float16, core.bfloat16) or b.type.dtype is not dt:
+            return None
+        if c.type.dtype is not core.float32:
+            return None
+        step = op.operands[2]
+        bm, bk = a.type.shape
+        bn = b.type.shape[1]
+        if not (step.op is not None and step.op.name == "const" and step.op.attrs["value"] == bk):
+            return None
+        plan = self.dot_plans[dot.result.id]
+        if plan.inst.m != 32 or plan.inst.k != 16 or plan.wrep != 1:
+            return None
+        nt = self.nt
+        kc = bk // 8
+        if bk % 16 or (bm * kc) % nt or ((kc * (bn // 8)) % nt and kc * (bn // 8) >= nt):
+            return None
+        if self.lay[acc.id].key() != LY.mfma_acc(plan).key():
+            return None
+        A, B = self.desc[da.id], self.desc[db.id]
+        ok = lambda v, d: self.axis.get(v).div[0] >= d  # noqa: E731
+        if not (ok(A["base_v"], 16) and ok(B["base_v"], 16) and ok(A["stride_v"][0], 8)
+                and ok(B["stride_v"][0], 8)):
+            return None
+        n0v = lb.operands[2]
+        return {"plan": plan, "A": A, "B": B, "m0": la.operands[1], "n0": n0v,
+                "scalar_ops": scalar_ops, "dt": dt, "bm": bm, "bn": bn, "bk": bk,
+                "n0_aligned": True}
+
+    def _emit_gemm_loop(self, op, g) -> bool:
+        body = op.regions[0]
+        acc_arg = body.args[1]
+        init = op.operands[3]
+        lo, hi = (self.name[o.id] for o in op.operands[:2])
+        lay = self.lay[acc_arg.id]
+        nm = self.fresh("c")
+        self.emit(f"float {nm}[{lay.nregs}];")
+        self.emit("#pragma unroll")
+        self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = {self.elem(init, lay, 'r')};")
+        self.emit("{")
+        # loop-invariant scalar ops of the body (offsets), evaluated once
+        for o in g["scalar_ops"]:
+            self.gen_op(o)
+        p = g["plan"]
+        T = ctype(g["dt"])
+        A, B = g["A"], g["B"]
+        tmpl = f"ek::Gemm<{T}, {g['bm']}, {g['bn']}, {g['bk']}, {p.wm}, {p.wn}, {self.nt}>"
+        lds = 2 * (g["bm"] + g["bn"]) * g["bk"] * 2
+        self.need_lds(lds)
+        self.emit(f"  {tmpl} ek_g;")
+        self.emit(f"  ek_g.run({nm}, {A['base']}, {A['strides'][0]}, {B['base']}, "
+                  f"{B['strides'][0]}, {A['shape'][0]}, {B['shape'][1]}, {A['shape'][1]}, "
+                  f"{self.name[g['m0'].id]}, {self.name[g['n0'].id]}, {lo}, {hi}, ek_smem, ek_tid);")
+        self.emit("}")
+        self.define(op.results[0], nm)
+        self.uses_template = True
+        self.big_acc = max(getattr(self, "big_acc", 0), lay.nregs)
+        return True
+
     # -- control flow -----------------------------------------------------------------
     def op_for(self, op):
+        if not self.opt.get("no_gemm_template"):
+            g = self._gemm_match(op)
+            if g is not None and self._emit_gemm_loop(op, g):
+                return
         body = op.regions[0]
         iv, carried = body.args[0], body.args[1:]
         lo, hi, step = (self.name[o.id] for o in op.operands[:3])
@@ -1456,10 +1567,14 @@ class Emitter:
                 self.name[a.id] = f"a{i}" if not dt.is_bool() else f"((bool)a{i})"
             self.def_level[a.id] = 0
         self.assign_block(fn.body)
+        self.remap_pids = bool(self.dot_plans) and not self.opt.get("no_pid_remap")
         self.gen_block(fn.body)
         kname = f"ek_{fn.name}"
         out = ['#include "enceladus_cdna4.h"', ""]
-        out.append(f'extern "C" __global__ void __launch_bounds__({self.nt}) {kname}('
+        attrs = f"__launch_bounds__({self.nt})"
+        if getattr(self, "big_acc", 0) >= 128:
+            attrs += " __attribute__((amdgpu_waves_per_eu(1, 1)))"
+        out.append(f'extern "C" __global__ void {attrs} {kname}('
                    + ", ".join(params) + ") {")
         if self.lds:
             lds = (self.lds + 15) // 16 * 16
@@ -1468,6 +1583,8 @@ class Emitter:
         out.append("  const int ek_lane = ek_tid & 63;")
         out.append("  const int ek_warp = ek_tid >> 6;")
         out.append("  (void)ek_lane; (void)ek_warp; (void)ek_tid;")
+        if self.remap_pids:
+            out.extend(PID_REMAP)
         out.extend(self.prologue)
 
         def flat(items):
@@ -1479,6 +1596,27 @@ class Emitter:
         out.extend(flat(self.scopes[0].items))
         out.append("}")
         return GeneratedKernel(kname, "\n".join(out) + "\n", args, self.nw, self.lds, self.nt)
+
+
+# Program-id remapping for kernels with tl.dot (programs are independent, so any bijection
+# of program ids is allowed). Hardware hands consecutive workgroups to the 8 XCDs round
+# robin; remapping makes the programs on one XCD consecutive, grouped in bands of 4 rows of
+# axis 1, so they share operand tiles in that XCD's L2. Axis 0 runs in reverse so that in
+# causal attention the longest programs start first.
+PID_REMAP = [
+    "  int ek_pid_x, ek_pid_y;",
+    "  const int ek_pid_z = blockIdx.z;",
+    "  {",
+    "    const int gx = gridDim.x, gy = gridDim.y, nb = gx * gy;",
+    "    int L = blockIdx.x + gx * blockIdx.y;",
+    "    if ((nb & 7) == 0) L = (L & 7) * (nb >> 3) + (L >> 3);",
+    "    const int band = 4 * gx, first = (L / band) * 4;",
+    "    const int gs = (gy - first) < 4 ? (gy - first) : 4, r = L % band;",
+    "    ek_pid_y = first + r % gs;",
+    "    ek_pid_x = gx - 1 - r / gs;",
+    "  }",
+    "  (void)ek_pid_x; (void)ek_pid_y; (void)ek_pid_z;",
+]
 
 
 def generate(fn: ir.Func, options: dict | None = None) -> GeneratedKernel:

@@ -9,14 +9,14 @@
 // The header is compiled by hiprtc; it uses only compiler builtins, no system headers.
 #pragma once
 
-typedef signed char int8_t;
-typedef unsigned char uint8_t;
-typedef short int16_t;
-typedef unsigned short uint16_t;
-typedef int int32_t;
-typedef unsigned int uint32_t;
-typedef long long int64_t;
-typedef unsigned long long uint64_t;
+typedef __INT8_TYPE__ int8_t;
+typedef __UINT8_TYPE__ uint8_t;
+typedef __INT16_TYPE__ int16_t;
+typedef __UINT16_TYPE__ uint16_t;
+typedef __INT32_TYPE__ int32_t;
+typedef __UINT32_TYPE__ uint32_t;
+typedef __INT64_TYPE__ int64_t;
+typedef __UINT64_TYPE__ uint64_t;
 
 #define EK_INLINE __device__ __attribute__((always_inline)) inline
 
@@ -316,5 +316,168 @@ EK_INLINE void mfma_32x32x2(float* acc, const float* a, const float* b) {
   c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[0], b[0], c, 0, 0, 0);
   unpack(acc, c);
 }
+
+
+// ---------------------------------------------------------------------------
+// Block GEMM main loop for `for k in range(lo, hi, BK): acc = dot(A.load([m0, k]),
+// B.load([k, n0]), acc)` with row-major 16-bit A [M, K] (lda) and B [K, N] (ldb).
+//
+// NT threads = WM x WN waves; each wave owns a (BM/WM) x (BN/WN) block of 32x32 MFMA tiles
+// (v_mfma_f32_32x32x16_{f16,bf16}). The accumulator is held in the emitter's MFMA layout:
+// acc[(tm * TN + tn) * 16 + j].
+//
+// Per iteration each thread prefetches its share of the next A and B tiles from global
+// memory into registers (16-byte loads), computes the current tile from LDS, then writes
+// the prefetched registers into the other LDS stage: one barrier per iteration.
+// LDS holds A as [BM][BK] and B transposed as [BN][BK], both with k contiguous and the
+// 16-byte chunk index XOR-swizzled by the row, so every MFMA operand is one 128-bit LDS
+// read. B is transposed in registers: each thread loads an 8x8 block (8 k rows x 8 n
+// columns) and permutes it with v_perm_b32 before writing 8 rows of B^T.
+// ---------------------------------------------------------------------------
+EK_INLINE uint32_t perm_lo(uint32_t lo_src, uint32_t hi_src) {
+  return __builtin_amdgcn_perm(hi_src, lo_src, 0x05040100u);  // (lo16(lo_src), lo16(hi_src))
+}
+EK_INLINE uint32_t perm_hi(uint32_t lo_src, uint32_t hi_src) {
+  return __builtin_amdgcn_perm(hi_src, lo_src, 0x07060302u);  // (hi16(lo_src), hi16(hi_src))
+}
+
+// r[j] holds 8 halves of row j (columns 0..7); o[i] receives column i (rows 0..7).
+EK_INLINE void transpose8x8(const u32x4* r, u32x4* o) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int w = i >> 1;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint32_t a = r[2 * q][w], b = r[2 * q + 1][w];
+      o[i][q] = (i & 1) ? perm_hi(a, b) : perm_lo(a, b);
+    }
+  }
+}
+
+template <typename T, int BM, int BN, int BK, int WM, int WN, int NT>
+struct Gemm {
+  static constexpr int TM = BM / WM / 32, TN = BN / WN / 32, TK = BK / 16;
+  static constexpr int KC = BK / 8;                    // 16-byte chunks per k row
+  static constexpr int SWZ = (KC < 8 ? KC : 8) - 1;    // xor mask for the chunk index
+  static constexpr int A_CH = BM * KC / NT;            // A chunks per thread
+  static constexpr int B_TOTAL = KC * (BN / 8);        // B 8x8 blocks per tile
+  static constexpr int B_BL = (B_TOTAL + NT - 1) / NT; // B 8x8 blocks per thread
+  static constexpr int STAGE = (BM + BN) * BK;         // elements per LDS stage
+  static constexpr int LDS_BYTES = 2 * STAGE * 2;
+  static_assert(TM >= 1 && TN >= 1 && TK >= 1, "tile too small for 32x32x16 MFMA");
+  static_assert((BM * KC) % NT == 0 && (B_TOTAL % NT == 0 || B_TOTAL < NT),
+                "tile/thread mismatch");
+  static_assert(WM * WN * 64 == NT, "warps must tile the block");
+
+  u32x4 ra[A_CH];
+  u32x4 rb[B_BL][8];
+
+  EK_INLINE void load(const uint16_t* A, int lda, const uint16_t* B, int ldb, int M, int N,
+                      int K, int m0, int n0, int k, int tid) {
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) {
+      const int c = tid + i * NT, row = c / KC, kc = c % KC;
+      const int gr = m0 + row, gk = k + kc * 8;
+      if (gr < M && gk + 8 <= K) {
+        ra[i] = *reinterpret_cast<const u32x4*>(A + (int64_t)gr * lda + gk);
+      } else {
+        uint16_t h[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          h[e] = (gr < M && gk + e < K && gk + e >= 0) ? A[(int64_t)gr * lda + gk + e] : 0;
+        __builtin_memcpy(&ra[i], h, 16);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < B_BL; ++i) {
+      const int b = tid + i * NT, nb = b % (BN / 8), kb = b / (BN / 8);
+      if (B_TOTAL < NT && b >= B_TOTAL) break;
+      const int gn = n0 + nb * 8;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int gk = k + kb * 8 + j;
+        if (gk < K && gn + 8 <= N) {
+          rb[i][j] = *reinterpret_cast<const u32x4*>(B + (int64_t)gk * ldb + gn);
+        } else {
+          uint16_t h[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            h[e] = (gk < K && gn + e < N) ? B[(int64_t)gk * ldb + gn + e] : 0;
+          __builtin_memcpy(&rb[i][j], h, 16);
+        }
+      }
+    }
+  }
+
+  EK_INLINE void store(uint16_t* st, int tid) {
+    uint16_t* sA = st;
+    uint16_t* sB = st + BM * BK;
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) {
+      const int c = tid + i * NT, row = c / KC, kc = c % KC;
+      *reinterpret_cast<u32x4*>(sA + row * BK + ((kc ^ (row & SWZ)) << 3)) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_BL; ++i) {
+      const int b = tid + i * NT, nb = b % (BN / 8), kb = b / (BN / 8);
+      if (B_TOTAL < NT && b >= B_TOTAL) break;
+      u32x4 o[8];
+      transpose8x8(rb[i], o);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int n = nb * 8 + q;
+        *reinterpret_cast<u32x4*>(sB + n * BK + ((kb ^ (n & SWZ)) << 3)) = o[q];
+      }
+    }
+  }
+
+  EK_INLINE void compute(float* acc, const uint16_t* st, int lane, int wm, int wn) {
+    const uint16_t* sA = st;
+    const uint16_t* sB = st + BM * BK;
+    const int r32 = lane & 31, h = lane >> 5;
+#pragma unroll
+    for (int kk = 0; kk < TK; ++kk) {
+      T a[TM][8], b[TN][8];
+      const int kc = kk * 2 + h;
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm) {
+        const int row = wm * (BM / WM) + tm * 32 + r32;
+        vload<T, 8>(a[tm], reinterpret_cast<const T*>(sA + row * BK + ((kc ^ (row & SWZ)) << 3)));
+      }
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+        const int col = wn * (BN / WN) + tn * 32 + r32;
+        vload<T, 8>(b[tn], reinterpret_cast<const T*>(sB + col * BK + ((kc ^ (col & SWZ)) << 3)));
+      }
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) mfma_32x32x16(&acc[(tm * TN + tn) * 16], a[tm], b[tn]);
+    }
+  }
+
+  // Runs the whole k loop: k = lo, lo + BK, ... < hi.
+  EK_INLINE void run(float* acc, const T* A, int lda, const T* B, int ldb, int M, int N, int K,
+                     int m0, int n0, int lo, int hi, char* smem, int tid) {
+    if (hi <= lo) return;
+    const int niter = (hi - lo + BK - 1) / BK;
+    const int lane = tid & 63, warp = tid >> 6;
+    const int wm = warp % WM, wn = warp / WM;
+    const uint16_t* A16 = reinterpret_cast<const uint16_t*>(A);
+    const uint16_t* B16 = reinterpret_cast<const uint16_t*>(B);
+    uint16_t* s16 = reinterpret_cast<uint16_t*>(smem);
+    __syncthreads();
+    load(A16, lda, B16, ldb, M, N, K, m0, n0, lo, tid);
+    store(s16, tid);
+    __syncthreads();
+    for (int it = 0; it < niter; ++it) {
+      const bool more = it + 1 < niter;
+      if (more) load(A16, lda, B16, ldb, M, N, K, m0, n0, lo + (it + 1) * BK, tid);
+      compute(acc, s16 + (it & 1) * STAGE, lane, wm, wn);
+      if (more) store(s16 + ((it + 1) & 1) * STAGE, tid);
+      __syncthreads();
+    }
+  }
+};
 
 }  // namespace ek

@@ -88,3 +88,33 @@ def test_literals_are_exact():
     assert codegen_hip.literal(float("inf"), core.float32) == "__builtin_inff()"
     assert codegen_hip.literal(1.0, core.bfloat16) == "ek::bf16{0x3f80}"
     assert codegen_hip.literal(-2147483648, core.int32).startswith("(int32_t)(-2147483647")
+
+
+def test_program_id_remap_is_a_bijection():
+    def remap(bx, by, gx, gy):
+        nb = gx * gy
+        L = bx + gx * by
+        if nb % 8 == 0:
+            L = (L % 8) * (nb // 8) + L // 8
+        band = 4 * gx
+        first = (L // band) * 4
+        gs = min(gy - first, 4)
+        r = L % band
+        return (gx - 1 - r // gs, first + r % gs)
+    src = "\n".join(codegen_hip.PID_REMAP)
+    assert "(L & 7) * (nb >> 3)" in src and "ek_pid_x = gx - 1 - r / gs" in src
+    for gx, gy in [(16, 16), (32, 128), (8, 1), (3, 5), (7, 9), (1, 1), (2, 100)]:
+        got = {remap(x, y, gx, gy) for x in range(gx) for y in range(gy)}
+        assert got == {(x, y) for x in range(gx) for y in range(gy)}
+
+
+def test_descriptor_dot_loop_uses_gemm_template():
+    from examples.matmul import matmul_desc_kernel
+    f16 = np.zeros(16, np.float16)
+    src = codegen_hip.generate(matmul_desc_kernel.ir_for(
+        f16, f16, f16, 4096, 4096, 4096, 4096, 4096, 4096, BM=256, BN=256, BK=64)).source
+    assert "ek::Gemm<_Float16, 256, 256, 64, 2, 2, 256>" in src
+    # unaligned strides fall back to the generic lowering
+    src2 = codegen_hip.generate(matmul_desc_kernel.ir_for(
+        f16, f16, f16, 100, 90, 70, 70, 90, 90, BM=64, BN=64, BK=32)).source
+    assert "ek::Gemm<" not in src2

@@ -157,3 +157,31 @@ def test_flash_attention_fp16(causal, n, d, bm, bn):
     got = attention(q, k, v, causal, block_m=bm, block_n=bn).astype(np.float64)
     want = R.attention(q, k, v, causal)
     np.testing.assert_allclose(got, want, rtol=2e-3, atol=2e-3)
+
+
+@pytest.mark.parametrize("m,n,k,bm,bn,bk,nw", [(512, 512, 256, 256, 256, 64, 4),
+                                                (256, 512, 128, 128, 256, 32, 4),
+                                                (512, 256, 192, 256, 128, 64, 4),
+                                                (512, 512, 128, 256, 256, 64, 8),
+                                                (320, 272, 200, 128, 128, 64, 4)])
+def test_matmul_gemm_template(m, n, k, bm, bn, bk, nw):
+    """The descriptor dot loop on the hand-written MFMA main loop, including ragged edges
+    (zero-filled A/B tiles) and K not a multiple of BK."""
+    from examples.matmul import matmul_desc
+    _say(f"matmul template {m}x{n}x{k} tile {bm}x{bn}x{bk} warps {nw}")
+    a, b = _half((m, k), 0, 1 / 8), _half((k, n), 1, 1 / 8)
+    got = matmul_desc(a, b, bm=bm, bn=bn, bk=bk, num_warps=nw).astype(np.float32)
+    want = R.matmul(a, b).astype(np.float32)
+    np.testing.assert_allclose(got, want, rtol=2e-3, atol=1e-3)
+
+
+def test_matmul_template_bf16_torch():
+    import torch
+    from examples.matmul import matmul_desc
+    _say("matmul template bf16 512^3")
+    g = torch.Generator().manual_seed(0)
+    a = (torch.randn(512, 512, generator=g) / 8).bfloat16()
+    b = (torch.randn(512, 512, generator=g) / 8).bfloat16()
+    c = matmul_desc(a.cuda(), b.cuda(), bm=256, bn=256, bk=64).float().cpu()
+    want = (a.float() @ b.float()).bfloat16().float()
+    np.testing.assert_allclose(c.numpy(), want.numpy(), rtol=1.6e-2, atol=1e-2)
