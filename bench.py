@@ -211,6 +211,19 @@ def w_cumsum(torch, timer, steps, warmup):
             "gbps": nbytes / ms / 1e6, "bound": "hbm", "kernel": launches[0].ck.name}
 
 
+def w_torch_matmul(torch, timer, steps, warmup):
+    """Calibration only: torch.matmul (hipBLASLt) on the same fp16 4096^3 problem."""
+    M = N = K = 4096
+    a = (torch.randn(M, K, device="cuda") / 64).half()
+    b = (torch.randn(K, N, device="cuda") / 64).half()
+    c = torch.empty(M, N, dtype=torch.float16, device="cuda")
+    ms = timer.run([lambda: torch.matmul(a, b, out=c)], max(5, steps // 2), 3)
+    flop = 2 * M * N * K
+    return {"name": "torch_matmul", "config": "hipBLASLt fp16 4096^3 (calibration, not ours)",
+            "ms": ms, "flop": flop, "tflops": flop / ms / 1e9, "bound": "mfma",
+            "kernel": "torch.matmul"}
+
+
 WORKLOADS = {
     "softmax": w_softmax, "rmsnorm": w_rmsnorm, "vector_add": w_vector_add,
     "matmul": lambda t, tm, s, w: w_matmul(t, tm, s, w, False),
@@ -218,6 +231,7 @@ WORKLOADS = {
     "attention_causal": lambda t, tm, s, w: w_attention(t, tm, s, w, True, 4096),
     "attention_noncausal": lambda t, tm, s, w: w_attention(t, tm, s, w, False, 1024),
     "histogram": w_histogram, "cumsum": w_cumsum,
+    "torch_matmul": w_torch_matmul,
 }
 
 

@@ -158,6 +158,7 @@ class Emitter:
         self.lds = 0
         self.dot_plans: dict[int, LY.DotPlan] = {}
         self.inplace: set[int] = set()
+        self.extra_smem: list[tuple[str, int]] = []
 
     # ------------------------------------------------------------------ utilities
     def fresh(self, hint="v") -> str:
@@ -173,6 +174,8 @@ class Emitter:
 
     def need_lds(self, nbytes: int):
         self.lds = max(self.lds, nbytes)
+        if getattr(self, "in_staged_loop", 0):
+            self.scratch_in_stage_loop = True
 
     def tile(self, v: ir.Value) -> bool:
         return not isinstance(v.type, ir.DescType) and v.type.shape != ()
@@ -220,8 +223,90 @@ class Emitter:
         for op in block.ops:
             self.assign_op(op)
 
+    # -- dot planning ------------------------------------------------------------------
+    _EW = ("binary", "unary", "cast", "select", "fma", "bitcast", "hint")
+
+    def _dot_source(self, v: ir.Value, depth=0):
+        """The dot whose accumulator `v` derives from elementwise (same shape), if any."""
+        if v.op is None or depth > 64:
+            return None
+        if v.op.name == "dot":
+            return v.op
+        if v.op.name in self._EW:
+            for o in v.op.operands:
+                if o.type.shape == v.type.shape:
+                    d = self._dot_source(o, depth + 1)
+                    if d is not None:
+                        return d
+        return None
+
+    def plan_dots(self, fn: ir.Func):
+        """Chooses warps/MFMA shape per dot, and the transposed orientation with a matching
+        k order when one dot's result feeds another dot's A operand (attention's P), so
+        the product's registers are the next MFMA's operand registers."""
+        dw = self.opt.get("dot_warps")
+        dots = [op for op in ir.walk(fn.body) if op.name == "dot"]
+        base = {}
+        for d in dots:
+            a, b = d.operands[0], d.operands[1]
+            try:
+                base[d] = LY.plan_dot(a.type.shape[0], b.type.shape[1], a.type.shape[1],
+                                      self.nw, a.type.dtype.name, dw)
+            except ValueError as e:
+                raise CompilationError(str(e)) from None
+        trans, korder = set(), {}
+        if not self.opt.get("no_dot_transpose"):
+            for d2 in dots:
+                d1 = self._dot_source(d2.operands[0])
+                if d1 is None or d1 is d2:
+                    continue
+                p1, p2 = base[d1], base[d2]
+                if p1.inst.m != 32 or p2.inst.m != 32 or p2.inst.k != 16:
+                    continue
+                if (p1.wm, p1.wn) != (p2.wm, p2.wn) or p1.wn != 1 or p1.bm != p2.bm:
+                    continue
+                trans.update((d1, d2))
+                nk = LY.log2(p2.bk)
+                if nk >= 4:
+                    korder[d2] = (0, 1, 3, 2) + tuple(range(4, nk))
+        for d in dots:
+            a, b = d.operands[0], d.operands[1]
+            self.dot_plans[d.result.id] = LY.plan_dot(
+                a.type.shape[0], b.type.shape[1], a.type.shape[1], self.nw, a.type.dtype.name,
+                dw, d in trans, korder.get(d, ()))
+
+    def _operand_layout_for(self, v: ir.Value):
+        """If `v`'s single use is a dot operand (directly or through trans), the layout that
+        operand wants, expressed in `v`'s own shape."""
+        us = self.uses.get(v.id, [])
+        if len(us) != 1:
+            return None
+        u = us[0]
+        perm = None
+        if u.name == "trans" and len(self.uses.get(u.result.id, [])) == 1:
+            perm = u.attrs["perm"]
+            v2 = u.result
+            u = self.uses[v2.id][0]
+        else:
+            v2 = v
+        if u.name != "dot":
+            return None
+        plan = self.dot_plans[u.result.id]
+        if u.operands[0].id == v2.id:
+            lay = LY.mfma_operand(plan, "a")
+        elif u.operands[1].id == v2.id:
+            lay = LY.mfma_operand(plan, "b")
+        else:
+            return None
+        if perm is not None:
+            inv = [0] * len(perm)
+            for i, p in enumerate(perm):
+                inv[p] = i
+            lay = lay.permute(tuple(inv))
+        return lay
+
     def _anch(self, v):
-        return self.kind.get(v.id) in ("anchored", "view")
+        return self.kind.get(v.id) in ("anchored", "view", "staged")
 
     def assign_op(self, op: ir.Op):
         n = op.name
@@ -286,19 +371,24 @@ class Emitter:
             if len(us) == 1 and us[0].name == "scan":
                 lay = LY.scan_layout(res.type.shape, us[0].attrs["axis"], self.nw)
             self.lay[res.id] = lay
+        elif n == "desc_load" and res.id in self.staged:
+            self.kind[res.id] = "staged"
+            self.lay[res.id] = self.staged[res.id]["lay"]
         elif n == "desc_load":
             self.kind[res.id] = "anchored"
             es = res.type.dtype.itemsize
-            self.lay[res.id] = LY.blocked(res.type.shape, LY.default_order(res.type.shape),
-                                          max(1, 16 // es), self.nw)
+            lay = self._operand_layout_for(res)
+            if lay is not None:
+                d, nb = lay.vec_dim_bits()
+                # direct operand loads only when each lane reads >= 16 contiguous bytes
+                if not (d == len(lay.shape) - 1 and (1 << nb) * es >= 16):
+                    lay = None
+            if lay is None:
+                lay = LY.blocked(res.type.shape, LY.default_order(res.type.shape),
+                                 max(1, 16 // es), self.nw)
+            self.lay[res.id] = lay
         elif n == "dot":
-            a, b = op.operands[0], op.operands[1]
-            try:
-                plan = LY.plan_dot(a.type.shape[0], b.type.shape[1], a.type.shape[1], self.nw,
-                                   a.type.dtype.name, self.opt.get("dot_warps"))
-            except ValueError as e:
-                raise CompilationError(str(e)) from None
-            self.dot_plans[op.result.id] = plan
+            plan = self.dot_plans[op.result.id]
             self.kind[res.id] = "anchored"
             self.lay[res.id] = LY.mfma_acc(plan)
         elif n == "reduce":
@@ -564,6 +654,8 @@ class Emitter:
         src, sl, ri = self.resolve(v, lay, r)
         if self.kind.get(src.id) == "cheap":
             return self.cheap(src, [self.coord(sl, d, ri) for d in range(len(sl.shape))])
+        if self.kind.get(src.id) == "staged":
+            return f"{self.read_staged(src, sl)}[{ri}]"
         a = self.lay[src.id]
         nm = self.name[src.id]
         if a.key() == sl.key():
@@ -576,6 +668,12 @@ class Emitter:
     def array(self, v: ir.Value, lay: LY.Layout) -> str:
         """Name of an array holding `v` in exactly `lay` (materialising if needed)."""
         k = self.kind.get(v.id)
+        if k == "staged":
+            return self.read_staged(v, lay)
+        if k == "view":
+            src, sl, ri = self.resolve(v, lay, "r")
+            if self.kind.get(src.id) == "staged" and ri == "r":
+                return self.read_staged(src, sl)
         if k == "anchored" and self.lay[v.id].key() == lay.key():
             return self.name[v.id]
         if k in ("anchored", "view"):
@@ -594,14 +692,17 @@ class Emitter:
         return nm
 
     # ------------------------------------------------------------------ LDS conversion
-    def lds_order(self, a: LY.Layout, b: LY.Layout):
+    def lds_order(self, a: LY.Layout, b: LY.Layout, es: int = 4):
         rank = len(a.shape)
-        da, na = a.vec_dim_bits()
-        db, nb = b.vec_dim_bits()
-        f = db if nb >= na else da
         if rank == 0:
             return []
-        return [f] + [d for d in reversed(range(rank)) if d != f]
+        best = None
+        for f in dict.fromkeys([b.vec_dim_bits()[0], a.vec_dim_bits()[0]]):
+            order = [f] + [d for d in reversed(range(rank)) if d != f]
+            cost = a.nregs // self.lds_vec(a, order, es) + b.nregs // self.lds_vec(b, order, es)
+            if best is None or cost < best[0]:
+                best = (cost, order)
+        return best[1]
 
     def lds_addr(self, shape, order, es: int):
         """Strides (elements) for an LDS image of `shape` with the given dim order,
@@ -647,7 +748,7 @@ class Emitter:
         a = self.lay[src.id]
         t = ctype(src.type.dtype) + ("*" if src.type.ptr else "")
         es = 8 if src.type.ptr else src.type.dtype.itemsize
-        order = self.lds_order(a, dst)
+        order = self.lds_order(a, dst, es)
         strides, total = self.lds_addr(a.shape, order, es)
         nbytes = total * es
         if nbytes > MAX_LDS:
@@ -891,6 +992,9 @@ class Emitter:
         return " + ".join(idx), " && ".join(conds)
 
     def op_desc_load(self, op):
+        if op.result.id in getattr(self, "staged", {}):
+            self.def_level[op.result.id] = len(self.scopes) - 1
+            return
         desc, offs = op.operands[0], op.operands[1:]
         d = self.desc[desc.id]
         res = op.result
@@ -1290,6 +1394,35 @@ class Emitter:
         return "(" + " + ".join(terms) + ")" if terms else "0"
 
     # -- dot --------------------------------------------------------------------------
+    def _staged_operand(self, v: ir.Value, lay: LY.Layout):
+        """(info, layout over the staged tile) when `v` is a staged tile or a view of one."""
+        k = self.kind.get(v.id)
+        if k == "staged":
+            return self.staged[v.id], lay
+        if k == "view":
+            src, sl, ri = self.resolve(v, lay, "r")
+            if self.kind.get(src.id) == "staged" and ri == "r":
+                return self.staged[src.id], sl
+        return None
+
+    def _frag_read(self, info, lay: LY.Layout, first: str, n: int, dst: str, decl=True):
+        """Emits LDS reads of registers [first, first+n) of `lay` from a staged tile."""
+        T = info["T"]
+        d, nb = lay.vec_dim_bits()
+        want = 1 if info["mode"] == "row" else 0
+        V = min(1 << nb, 8, n) if d == want else 1
+        sm = (f"(reinterpret_cast<const {T}*>({info['smem']}) + (ek_it{info['loop_idx']} & 1) * "
+              f"{info['stage_elems']})")
+        r = f"({first} + j)"
+        r0, r1 = self.coord(lay, 0, r), self.coord(lay, 1, r)
+        idx = f"({r0}) * {info['pitch']} + ({r1})" if info["mode"] == "row" else \
+            f"({r1}) * {info['pitch']} + ({r0})"
+        if decl:
+            self.emit(f"      {T} {dst}[{n}];")
+        self.emit(f"    #pragma unroll")
+        self.emit(f"    for (int j = 0; j < {n}; j += {V}) ek::vload<{T}, {V}>(&{dst}[j], "
+                  f"&{sm}[{idx}]);")
+
     def op_dot(self, op):
         a, b, c = op.operands
         res = op.result
@@ -1297,8 +1430,10 @@ class Emitter:
         la, lb = LY.mfma_operand(plan, "a"), LY.mfma_operand(plan, "b")
         lc = self.lay[res.id]
         ins = plan.inst
-        aa = self.array(a, la)
-        bb = self.array(b, lb)
+        sa = self._staged_operand(a, la)
+        sb = self._staged_operand(b, lb)
+        aa = None if sa else self.array(a, la)
+        bb = None if sb else self.array(b, lb)
         cdt = res.type.dtype
         nacc = 16 if ins.m == 32 else 4
         single = len(self.uses.get(c.id, [])) == 1
@@ -1312,14 +1447,37 @@ class Emitter:
             self.emit(f"for (int r = 0; r < {lc.nregs}; ++r) {nm}[r] = "
                       f"ek::f32({self.elem(c, lc, 'r')});")
         tm, tn, tk, kpl = plan.tm, plan.tn, plan.tk, ins.kpl
+        # Per k step: read every A and B fragment first (staged operands come from LDS),
+        # then issue the TM x TN MFMAs, so LDS latency overlaps the previous step's MFMAs.
         self.emit("#pragma unroll")
         self.emit(f"for (int kk = 0; kk < {tk}; ++kk) {{")
+        if sa:
+            T = sa[0]["T"]
+            self.emit(f"  {T} fa[{tm}][{kpl}];")
+            self.emit("  #pragma unroll")
+            self.emit(f"  for (int im = 0; im < {tm}; ++im) {{")
+            self._frag_read(sa[0], sa[1], f"(im * {tk} + kk) * {kpl}", kpl, "fa[im]", decl=False)
+            self.emit("  }")
+            ea = "fa[im]"
+        else:
+            ea = f"&{aa}[(im * {tk} + kk) * {kpl}]"
+        if sb:
+            T = sb[0]["T"]
+            self.emit(f"  {T} fb[{tn}][{kpl}];")
+            self.emit("  #pragma unroll")
+            self.emit(f"  for (int in_ = 0; in_ < {tn}; ++in_) {{")
+            self._frag_read(sb[0], sb[1], f"(in_ * {tk} + kk) * {kpl}", kpl, "fb[in_]",
+                            decl=False)
+            self.emit("  }")
+            eb = "fb[in_]"
+        else:
+            eb = f"&{bb}[(in_ * {tk} + kk) * {kpl}]"
+        x, y = (eb, ea) if plan.trans else (ea, eb)
         self.emit("  #pragma unroll")
-        self.emit(f"  for (int im = 0; im < {tm}; ++im) {{")
+        self.emit(f"  for (int im = 0; im < {tm}; ++im)")
         self.emit("    #pragma unroll")
-        self.emit(f"    for (int in_ = 0; in_ < {tn}; ++in_) ek::{ins.fn}(&{nm}[(im * {tn} + in_) "
-                  f"* {nacc}], &{aa}[(im * {tk} + kk) * {kpl}], &{bb}[(in_ * {tk} + kk) * {kpl}]);")
-        self.emit("  }")
+        self.emit(f"    for (int in_ = 0; in_ < {tn}; ++in_) "
+                  f"ek::{ins.fn}(&{nm}[(im * {tn} + in_) * {nacc}], {x}, {y});")
         self.emit("}")
         if cdt is not core.float32:
             out = self.fresh("acch")
@@ -1328,6 +1486,190 @@ class Emitter:
                       f"({nm}[r]);")
             nm = out
         self.define(res, nm)
+
+    # -- staged dot operands --------------------------------------------------------------
+    def plan_staging(self, block: ir.Block):
+        """Marks descriptor loads inside `for` loops that feed a tl.dot operand and whose
+        block offsets are the loop variable or loop-invariant. Those tiles go through a
+        double-buffered LDS stage: the next iteration's tile is loaded into registers at the
+        top of the body, stored to the other stage at the end, one barrier per iteration;
+        the dot reads its operand fragments straight from LDS ("row" stages keep the tile's
+        contiguous dim; "trans" stages transpose 8x8 blocks in registers on the way in)."""
+        if not hasattr(self, "staged"):
+            self.staged: dict[int, dict] = {}
+            self.stage_loops: dict[int, list] = {}
+        for op in block.ops:
+            for r in op.regions:
+                self.plan_staging(r)
+            if op.name != "for" or self.opt.get("no_staging"):
+                continue
+            body = op.regions[0]
+            iv = body.args[0]
+            inner = set()
+            for o in ir.walk(body):
+                inner.update(r.id for r in o.results)
+            inner.update(a.id for a in body.args)
+            found = []
+            for ld in body.ops:
+                if ld.name != "desc_load":
+                    continue
+                desc, offs = ld.operands[0], ld.operands[1:]
+                if desc.id in inner or len(offs) != 2:
+                    continue
+                kinds = []
+                for o in offs:
+                    if o.id == iv.id:
+                        kinds.append("iv")
+                    elif o.id not in inner:
+                        kinds.append("inv")
+                    elif o.op is not None and o.op.name == "const":
+                        kinds.append("const")
+                    else:
+                        kinds = None
+                        break
+                if kinds is None:
+                    continue
+                res = ld.result
+                if res.type.dtype.itemsize != 2:
+                    continue
+                lay = self._operand_layout_for(res)
+                if lay is None:
+                    continue
+                d, nb = lay.vec_dim_bits()
+                R, C = res.type.shape
+                if d == 1 and nb >= 2:
+                    mode = "row"
+                elif d == 0 and nb >= 2 and R % 8 == 0 and C % 8 == 0:
+                    mode = "trans"
+                else:
+                    continue
+                info = {"op": ld, "lay": lay, "mode": mode, "kinds": kinds, "R": R, "C": C,
+                        "loop": op}
+                self.staged[res.id] = info
+                found.append(info)
+            if found:
+                self.stage_loops[id(op)] = found
+
+    def _stage_offsets(self, info, kval: str):
+        vals = []
+        for o, k in zip(info["op"].operands[1:], info["kinds"]):
+            if k == "iv":
+                vals.append(kval)
+            elif k == "const":
+                vals.append(str(int(o.op.attrs["value"])))
+            else:
+                vals.append(self.name[o.id])
+        return vals
+
+    def _stage_setup(self, info, idx: int):
+        ld = info["op"]
+        d = self.desc[ld.operands[0].id]
+        R, C = info["R"], info["C"]
+        T = ctype(ld.result.type.dtype)
+        if info["mode"] == "row":
+            pitch = C + 8
+            stage_elems = R * pitch
+            nvec = R * C // 8
+        else:
+            pitch = R + 8
+            stage_elems = C * pitch
+            W = 8 if (R // 8) * (C // 8) >= self.nt or C % 4 else 4
+            info["W"] = W
+            nvec = (R // 8) * (C // W)
+        per = (nvec + self.nt - 1) // self.nt
+        name = f"ek_stg{idx}"
+        info.update({"desc": d, "T": T, "pitch": pitch, "stage_elems": stage_elems,
+                     "nvec": nvec, "per": per, "smem": name, "regs": f"ek_pf{idx}"})
+        self.extra_smem.append((name, 2 * stage_elems * 2))
+        if info["mode"] == "trans" and info["W"] == 4:
+            self.emit(f"ek::u32x2 {info['regs']}[{per * 8}];")
+        else:
+            regs = per * (8 if info["mode"] == "trans" else 1)
+            self.emit(f"ek::u32x4 {info['regs']}[{regs}];")
+
+    def _stage_load(self, info, kval: str) -> list[str]:
+        d = info["desc"]
+        o0, o1 = self._stage_offsets(info, kval)
+        C, per, nvec = info["C"], info["per"], info["nvec"]
+        base, s0 = d["base"], d["strides"][0]
+        sh0, sh1 = d["shape"][0], d["shape"][1]
+        regs = info["regs"]
+        out = ["#pragma unroll", f"for (int i = 0; i < {per}; ++i) {{",
+               f"  const int c = ek_tid + i * {self.nt};"]
+        if nvec % self.nt:
+            out.append(f"  if (c >= {nvec}) break;")
+        scalar = (f"(unsigned)gr < (unsigned){sh0} && (unsigned)(gc + e) < (unsigned){sh1}) ? "
+                  f"reinterpret_cast<const uint16_t*>({base})[(int64_t)gr * {s0} + gc + e] : "
+                  f"(uint16_t)0;")
+        if info["mode"] == "row":
+            out += [f"  const int r = c / {C // 8}, cc = (c % {C // 8}) * 8;",
+                    f"  const int gr = {o0} + r, gc = {o1} + cc;",
+                    f"  if ((unsigned)gr < (unsigned){sh0} && gc >= 0 && gc + 8 <= {sh1}) "
+                    f"{regs}[i] = *reinterpret_cast<const ek::u32x4*>({base} + (int64_t)gr * {s0} + gc);",
+                    "  else {", "    uint16_t h[8];",
+                    f"    for (int e = 0; e < 8; ++e) h[e] = ({scalar}",
+                    f"    __builtin_memcpy(&{regs}[i], h, 16);", "  }"]
+        else:
+            W = info["W"]
+            vt = "ek::u32x4" if W == 8 else "ek::u32x2"
+            out += [f"  const int rb = (c / {C // W}) * 8, cb = (c % {C // W}) * {W};",
+                    f"  const int gc = {o1} + cb;",
+                    "  #pragma unroll", "  for (int j = 0; j < 8; ++j) {",
+                    f"    const int gr = {o0} + rb + j;",
+                    f"    if ((unsigned)gr < (unsigned){sh0} && gc >= 0 && gc + {W} <= {sh1}) "
+                    f"{regs}[i * 8 + j] = *reinterpret_cast<const {vt}*>({base} + (int64_t)gr * {s0} + gc);",
+                    "    else {", f"      uint16_t h[{W}];",
+                    f"      for (int e = 0; e < {W}; ++e) h[e] = ({scalar}",
+                    f"      __builtin_memcpy(&{regs}[i * 8 + j], h, {2 * W});", "    }", "  }"]
+        out.append("}")
+        return out
+
+    def _stage_store(self, info, stage: str) -> list[str]:
+        C, per, nvec = info["C"], info["per"], info["nvec"]
+        regs, pitch = info["regs"], info["pitch"]
+        sm = f"(reinterpret_cast<uint16_t*>({info['smem']}) + ({stage}) * {info['stage_elems']})"
+        out = ["#pragma unroll", f"for (int i = 0; i < {per}; ++i) {{",
+               f"  const int c = ek_tid + i * {self.nt};"]
+        if nvec % self.nt:
+            out.append(f"  if (c >= {nvec}) break;")
+        if info["mode"] == "row":
+            out += [f"  const int r = c / {C // 8}, cc = (c % {C // 8}) * 8;",
+                    f"  *reinterpret_cast<ek::u32x4*>({sm} + r * {pitch} + cc) = {regs}[i];"]
+        else:
+            W = info["W"]
+            out += [f"  const int rb = (c / {C // W}) * 8, cb = (c % {C // W}) * {W};",
+                    f"  ek::u32x4 o[{W}];",
+                    f"  ek::transpose8x{W}(&{regs}[i * 8], o);",
+                    "  #pragma unroll",
+                    f"  for (int q = 0; q < {W}; ++q) *reinterpret_cast<ek::u32x4*>({sm} + "
+                    f"(cb + q) * {pitch} + rb) = o[q];"]
+        out.append("}")
+        return out
+
+    def read_staged(self, v: ir.Value, lay: LY.Layout) -> str:
+        key = ("stg", v.id, lay.key())
+        for sc in reversed(self.scopes):
+            if key in sc.memo:
+                return sc.memo[key]
+        info = self.staged[v.id]
+        T = info["T"]
+        d, nb = lay.vec_dim_bits()
+        want = 1 if info["mode"] == "row" else 0
+        V = min(1 << nb, 8) if d == want else 1
+        sm = (f"(reinterpret_cast<const {T}*>({info['smem']}) + (ek_it{info['loop_idx']} & 1) * "
+              f"{info['stage_elems']})")
+        r0, r1 = self.coord(lay, 0, "r"), self.coord(lay, 1, "r")
+        if info["mode"] == "row":
+            idx = f"({r0}) * {info['pitch']} + ({r1})"
+        else:
+            idx = f"({r1}) * {info['pitch']} + ({r0})"
+        nm = self.fresh("sr")
+        self.emit(f"{T} {nm}[{lay.nregs}];")
+        self.emit("#pragma unroll")
+        self.emit(f"for (int r = 0; r < {lay.nregs}; r += {V}) ek::vload<{T}, {V}>(&{nm}[r], "
+                  f"&{sm}[{idx}]);")
+        self.cur.memo[key] = nm
+        return nm
 
     # -- dot loops on the GEMM template ---------------------------------------------------
     def _gemm_match(self, op):
@@ -1388,7 +1730,7 @@ class Emitter:
         if not (step.op is not None and step.op.name == "const" and step.op.attrs["value"] == bk):
             return None
         plan = self.dot_plans[dot.result.id]
-        if plan.inst.m != 32 or plan.inst.k != 16 or plan.wrep != 1:
+        if plan.inst.m != 32 or plan.inst.k != 16 or plan.wrep != 1 or plan.trans:
             return None
         nt = self.nt
         kc = bk // 8
@@ -1401,10 +1743,8 @@ class Emitter:
         if not (ok(A["base_v"], 16) and ok(B["base_v"], 16) and ok(A["stride_v"][0], 8)
                 and ok(B["stride_v"][0], 8)):
             return None
-        n0v = lb.operands[2]
-        return {"plan": plan, "A": A, "B": B, "m0": la.operands[1], "n0": n0v,
-                "scalar_ops": scalar_ops, "dt": dt, "bm": bm, "bn": bn, "bk": bk,
-                "n0_aligned": True}
+        return {"plan": plan, "A": A, "B": B, "m0": la.operands[1], "n0": lb.operands[2],
+                "scalar_ops": scalar_ops, "dt": dt, "bm": bm, "bn": bn, "bk": bk}
 
     def _emit_gemm_loop(self, op, g) -> bool:
         body = op.regions[0]
@@ -1417,22 +1757,19 @@ class Emitter:
         self.emit("#pragma unroll")
         self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = {self.elem(init, lay, 'r')};")
         self.emit("{")
-        # loop-invariant scalar ops of the body (offsets), evaluated once
         for o in g["scalar_ops"]:
             self.gen_op(o)
         p = g["plan"]
         T = ctype(g["dt"])
         A, B = g["A"], g["B"]
         tmpl = f"ek::Gemm<{T}, {g['bm']}, {g['bn']}, {g['bk']}, {p.wm}, {p.wn}, {self.nt}>"
-        lds = 2 * (g["bm"] + g["bn"]) * g["bk"] * 2
-        self.need_lds(lds)
+        self.need_lds(2 * (g["bm"] + g["bn"]) * g["bk"] * 2)
         self.emit(f"  {tmpl} ek_g;")
         self.emit(f"  ek_g.run({nm}, {A['base']}, {A['strides'][0]}, {B['base']}, "
                   f"{B['strides'][0]}, {A['shape'][0]}, {B['shape'][1]}, {A['shape'][1]}, "
                   f"{self.name[g['m0'].id]}, {self.name[g['n0'].id]}, {lo}, {hi}, ek_smem, ek_tid);")
         self.emit("}")
         self.define(op.results[0], nm)
-        self.uses_template = True
         self.big_acc = max(getattr(self, "big_acc", 0), lay.nregs)
         return True
 
@@ -1461,11 +1798,44 @@ class Emitter:
                           f"{self.elem(i, lay, 'r')};")
         it = ctype(iv.type.dtype)
         ivn = self.fresh("iv")
+        stg = self.stage_loops.get(id(op), []) if hasattr(self, "stage_loops") else []
+        if stg:
+            li = self.counter
+            self.emit(f"int ek_it{li} = 0;")
+            for k, info in enumerate(stg):
+                info["loop_idx"] = li
+                self._stage_setup(info, len(self.extra_smem))
+            self.emit("__syncthreads();")
+            self.emit(f"if ({lo} < {hi}) {{")
+            for info in stg:
+                for ln in self._stage_load(info, lo):
+                    self.emit("  " + ln)
+                for ln in self._stage_store(info, "0"):
+                    self.emit("  " + ln)
+            self.emit("}")
+            self.emit("__syncthreads();")
         self.push_scope(f"for ({it} {ivn} = {lo}; {ivn} < {hi}; {ivn} += {step}) {{")
         self.define(iv, ivn)
         for a, nm in zip(carried, names):
             self.define(a, nm)
+        if stg:
+            self.in_staged_loop = getattr(self, "in_staged_loop", 0) + 1
+            self.emit(f"const bool ek_more{li} = {ivn} + {step} < {hi};")
+            self.emit(f"if (ek_more{li}) {{")
+            for info in stg:
+                for ln in self._stage_load(info, f"({ivn} + {step})"):
+                    self.emit("  " + ln)
+            self.emit("}")
         self.gen_block(body)
+        if stg:
+            self.emit(f"if (ek_more{li}) {{")
+            for info in stg:
+                for ln in self._stage_store(info, f"(ek_it{li} + 1) & 1"):
+                    self.emit("  " + ln)
+            self.emit("}")
+            self.emit("__syncthreads();")
+            self.emit(f"++ek_it{li};")
+            self.in_staged_loop -= 1
         y = body.ops[-1]
         self._assign_yield(y.operands, carried, names)
         self.pop_scope()
@@ -1566,6 +1936,8 @@ class Emitter:
                 params.append(f"{cp} a{i}")
                 self.name[a.id] = f"a{i}" if not dt.is_bool() else f"((bool)a{i})"
             self.def_level[a.id] = 0
+        self.plan_dots(fn)
+        self.plan_staging(fn.body)
         self.assign_block(fn.body)
         self.remap_pids = bool(self.dot_plans) and not self.opt.get("no_pid_remap")
         self.gen_block(fn.body)
@@ -1574,11 +1946,27 @@ class Emitter:
         attrs = f"__launch_bounds__({self.nt})"
         if getattr(self, "big_acc", 0) >= 128:
             attrs += " __attribute__((amdgpu_waves_per_eu(1, 1)))"
+        elif self.dot_plans and self.nt <= 256 and not self.opt.get("no_occupancy_hint"):
+            # Two waves per SIMD for MFMA loops: the second wave covers LDS and barrier
+            # latency. hiprtc otherwise settles on one wave when it can use >256 registers.
+            attrs += " __attribute__((amdgpu_waves_per_eu(2)))"
         out.append(f'extern "C" __global__ void {attrs} {kname}('
                    + ", ".join(params) + ") {")
-        if self.lds:
-            lds = (self.lds + 15) // 16 * 16
-            out.append(f"  __shared__ __attribute__((aligned(16))) char ek_smem[{lds}];")
+        # Stage buffers share the LDS block with the scratch used for conversions and
+        # reductions when no scratch user runs inside a staged loop (the stage prologue and
+        # every scratch user start with a barrier); otherwise they follow the scratch.
+        scratch = (self.lds + 15) // 16 * 16
+        off = 0 if not getattr(self, "scratch_in_stage_loop", False) else scratch
+        stage_offs = []
+        for nm_, nb_ in self.extra_smem:
+            stage_offs.append((nm_, off))
+            off += (nb_ + 15) // 16 * 16
+        total = max(scratch, off)
+        if total:
+            out.append(f"  __shared__ __attribute__((aligned(16))) char ek_smem[{total}];")
+        for nm_, o_ in stage_offs:
+            out.append(f"  char* const {nm_} = ek_smem + {o_};")
+        self.lds = total
         out.append("  const int ek_tid = threadIdx.x;")
         out.append("  const int ek_lane = ek_tid & 63;")
         out.append("  const int ek_warp = ek_tid >> 6;")

@@ -308,6 +308,8 @@ class DotPlan:
     wrep: int    # extra warps holding copies (when the tile is too small)
     inst: MfmaShape
     num_warps: int
+    trans: bool = False   # compute C^T = B^T A^T: M on lanes in the accumulator
+    korder: tuple = ()    # k-coordinate bits in operand order (reg, lane-group, k-step)
 
     @property
     def tm(self) -> int:
@@ -323,7 +325,7 @@ class DotPlan:
 
 
 def plan_dot(bm: int, bn: int, bk: int, num_warps: int, dtype_name: str,
-             dot_warps=None) -> DotPlan:
+             dot_warps=None, trans: bool = False, korder: tuple = ()) -> DotPlan:
     wb = log2(num_warps)
     if dot_warps is not None:
         wm, wn = int(dot_warps[0]), int(dot_warps[1])
@@ -349,7 +351,9 @@ def plan_dot(bm: int, bn: int, bk: int, num_warps: int, dtype_name: str,
     inst = pick_mfma(bm // wm, bn // wn, bk, dtype_name)
     if bk % inst.k:
         raise ValueError(f"tl.dot depth {bk} isn't a multiple of the MFMA depth {inst.k}")
-    return DotPlan(bm, bn, bk, wm, wn, wrep, inst, num_warps)
+    nk = log2(bk)
+    korder = tuple(korder) if korder else tuple(range(nk))
+    return DotPlan(bm, bn, bk, wm, wn, wrep, inst, num_warps, trans, korder)
 
 
 def _warp_bits(plan: DotPlan, m_bits: list, n_bits: list) -> tuple:
@@ -374,6 +378,11 @@ def mfma_acc(plan: DotPlan) -> Layout:
         inst_reg = [(0, 0), (0, 1)]
         lane = [(1, 0), (1, 1), (1, 2), (1, 3), (0, 2), (0, 3)]
         row_inst_bits, col_inst_bits = 4, 4
+    if plan.trans:
+        # The instruction produces C^T: its rows are our columns and vice versa.
+        sw = lambda b: (1 - b[0], b[1])  # noqa: E731
+        inst_reg = [sw(b) for b in inst_reg]
+        lane = [sw(b) for b in lane]
     tm_bits = [(0, row_inst_bits + t) for t in range(log2(plan.tm))]
     tn_bits = [(1, col_inst_bits + t) for t in range(log2(plan.tn))]
     m_w = [(0, row_inst_bits + log2(plan.tm) + t) for t in range(log2(plan.wm))]
@@ -395,6 +404,7 @@ def mfma_operand(plan: DotPlan, which: str) -> Layout:
     kb = log2(i.kpl)                 # k bits held in registers per lane
     row_bits = log2(i.m)             # lane bits for the row/col index
     kgroup_bits = LANE_BITS - row_bits  # lane bits for k groups
+    ko = plan.korder
     if which == "a":
         kdim, rdim = 1, 0
         tiles, wr = plan.tm, plan.wm
@@ -402,10 +412,10 @@ def mfma_operand(plan: DotPlan, which: str) -> Layout:
         kdim, rdim = 0, 1
         tiles, wr = plan.tn, plan.wn
     lane = [(rdim, t) for t in range(row_bits)]
-    lane += [(kdim, kb + t) for t in range(kgroup_bits)]
+    lane += [(kdim, ko[kb + t]) for t in range(kgroup_bits)]
     inst_k_bits = log2(i.k)
-    reg = [(kdim, t) for t in range(kb)]
-    reg += [(kdim, inst_k_bits + t) for t in range(log2(plan.tk))]
+    reg = [(kdim, ko[t]) for t in range(kb)]
+    reg += [(kdim, ko[inst_k_bits + t]) for t in range(log2(plan.tk))]
     reg += [(rdim, row_bits + t) for t in range(log2(tiles))]
     r_w = [(rdim, row_bits + log2(tiles) + t) for t in range(log2(wr))]
     # Warps: M warps first then N warps; an operand is shared by the other group.

@@ -354,6 +354,21 @@ EK_INLINE void transpose8x8(const u32x4* r, u32x4* o) {
   }
 }
 
+EK_INLINE void transpose8x8(const u32x4* r, u32x4* o, int) { transpose8x8(r, o); }
+
+// r[j] holds 4 halves of row j (columns 0..3); o[i] receives column i (rows 0..7).
+EK_INLINE void transpose8x4(const u32x2* r, u32x4* o) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int w = i >> 1;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint32_t a = r[2 * q][w], b = r[2 * q + 1][w];
+      o[i][q] = (i & 1) ? perm_hi(a, b) : perm_lo(a, b);
+    }
+  }
+}
+
 template <typename T, int BM, int BN, int BK, int WM, int WN, int NT>
 struct Gemm {
   static constexpr int TM = BM / WM / 32, TN = BN / WN / 32, TK = BK / 16;
@@ -409,13 +424,21 @@ struct Gemm {
     }
   }
 
+  // LDS addressing (in 16-byte chunks). A: row-major [BM][KC] chunks, chunk index xor'ed
+  // with (row >> 1) & 7, so 16 consecutive rows (reads) and 8 chunks x 2 rows (writes)
+  // each cover all 64 banks. B^T: k-chunk-major [KC][BN] chunks with the column
+  // permuted as n ^ ((n >> 4) & 7), so reads of 16 consecutive columns and writes of
+  // columns 8 apart (one per 8x8 block) are both conflict-free.
+  static EK_INLINE int a_chunk(int row, int kc) { return row * KC + (kc ^ ((row >> 1) & SWZ)); }
+  static EK_INLINE int b_chunk(int n, int kc) { return kc * BN + (n ^ ((n >> 4) & 7)); }
+
   EK_INLINE void store(uint16_t* st, int tid) {
-    uint16_t* sA = st;
-    uint16_t* sB = st + BM * BK;
+    u32x4* sA = reinterpret_cast<u32x4*>(st);
+    u32x4* sB = reinterpret_cast<u32x4*>(st + BM * BK);
 #pragma unroll
     for (int i = 0; i < A_CH; ++i) {
       const int c = tid + i * NT, row = c / KC, kc = c % KC;
-      *reinterpret_cast<u32x4*>(sA + row * BK + ((kc ^ (row & SWZ)) << 3)) = ra[i];
+      sA[a_chunk(row, kc)] = ra[i];
     }
 #pragma unroll
     for (int i = 0; i < B_BL; ++i) {
@@ -424,16 +447,13 @@ struct Gemm {
       u32x4 o[8];
       transpose8x8(rb[i], o);
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int n = nb * 8 + q;
-        *reinterpret_cast<u32x4*>(sB + n * BK + ((kb ^ (n & SWZ)) << 3)) = o[q];
-      }
+      for (int q = 0; q < 8; ++q) sB[b_chunk(nb * 8 + q, kb)] = o[q];
     }
   }
 
   EK_INLINE void compute(float* acc, const uint16_t* st, int lane, int wm, int wn) {
-    const uint16_t* sA = st;
-    const uint16_t* sB = st + BM * BK;
+    const u32x4* sA = reinterpret_cast<const u32x4*>(st);
+    const u32x4* sB = reinterpret_cast<const u32x4*>(st + BM * BK);
     const int r32 = lane & 31, h = lane >> 5;
 #pragma unroll
     for (int kk = 0; kk < TK; ++kk) {
@@ -441,13 +461,13 @@ struct Gemm {
       const int kc = kk * 2 + h;
 #pragma unroll
       for (int tm = 0; tm < TM; ++tm) {
-        const int row = wm * (BM / WM) + tm * 32 + r32;
-        vload<T, 8>(a[tm], reinterpret_cast<const T*>(sA + row * BK + ((kc ^ (row & SWZ)) << 3)));
+        const u32x4 v = sA[a_chunk(wm * (BM / WM) + tm * 32 + r32, kc)];
+        __builtin_memcpy(a[tm], &v, 16);
       }
 #pragma unroll
       for (int tn = 0; tn < TN; ++tn) {
-        const int col = wn * (BN / WN) + tn * 32 + r32;
-        vload<T, 8>(b[tn], reinterpret_cast<const T*>(sB + col * BK + ((kc ^ (col & SWZ)) << 3)));
+        const u32x4 v = sB[b_chunk(wn * (BN / WN) + tn * 32 + r32, kc)];
+        __builtin_memcpy(b[tn], &v, 16);
       }
 #pragma unroll
       for (int tm = 0; tm < TM; ++tm)
