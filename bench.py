@@ -87,6 +87,10 @@ MATMUL_CONFIGS = [(256, 256, 64, 4), (256, 256, 32, 4), (256, 128, 64, 4), (128,
                   (128, 128, 64, 4), (256, 256, 64, 8)]
 
 
+# (BLOCK_M, BLOCK_N, num_warps) swept for the attention rows (dot_warps = (num_warps, 1))
+ATTN_CONFIGS = [(128, 64, 4), (128, 128, 4), (128, 32, 4), (256, 64, 8), (256, 128, 8)]
+
+
 def sets_for(bytes_per_set):
     return max(2, math.ceil(600e6 / bytes_per_set))
 
@@ -173,12 +177,20 @@ def w_attention(torch, timer, steps, warmup, causal=True, n=4096):
     g = torch.Generator(device="cpu").manual_seed(0)
     q, k, v = (torch.randn(B, H, n, D, generator=g).bfloat16().cuda() for _ in range(3))
     o = torch.empty_like(q)
-    l = make_launch(attention_kernel, (n // 128, B * H), (q, k, v, o, D ** -0.5, n, n * D, D),
-                    HEAD_DIM=D, BLOCK_M=128, BLOCK_N=64, CAUSAL=causal, dot_warps=(4, 1))
-    ms = timer.run([l], max(3, steps // 4), max(1, warmup // 4))
+    best = None
+    for bm, bn, nw in ATTN_CONFIGS:
+        l = make_launch(attention_kernel, (n // bm, B * H), (q, k, v, o, D ** -0.5, n, n * D, D),
+                        HEAD_DIM=D, BLOCK_M=bm, BLOCK_N=bn, CAUSAL=causal, num_warps=nw,
+                        dot_warps=(nw, 1))
+        ms = timer.run([l], max(3, steps // 4), max(1, warmup // 4))
+        log(f"    BLOCK_M={bm} BLOCK_N={bn} warps={nw}: {ms * 1e3:.1f} us")
+        if best is None or ms < best[0]:
+            best = (ms, l, (bm, bn, nw))
+    ms, l, cfg = best
     flop = 4 * B * H * n * n * D // (2 if causal else 1)
     return {"name": f"attention_{'causal' if causal else 'noncausal'}_{n}",
-            "config": f"bf16 [4,32,{n},128] {'causal' if causal else 'non-causal'}", "ms": ms,
+            "config": f"bf16 [4,32,{n},128] {'causal' if causal else 'non-causal'} "
+                      f"BLOCK_M/N/warps={cfg}", "ms": ms,
             "flop": flop, "tflops": flop / ms / 1e9, "bound": "mfma", "kernel": l.ck.name}
 
 

@@ -39,7 +39,7 @@ from enceladus_amd.language import core
 
 MAX_LDS = 160 * 1024
 
-_MATH = {"exp": "expf", "exp2": "exp2f", "log": "logf", "log2": "log2f", "sqrt": "sqrtf",
+_MATH = {"exp": "expf", "exp2": "ek::exp2_fast", "log": "logf", "log2": "log2f", "sqrt": "sqrtf",
          "sin": "sinf", "cos": "cosf", "tanh": "tanhf", "erf": "erff", "floor": "floorf",
          "ceil": "ceilf"}
 _INFIX = {"add": "+", "sub": "-", "mul": "*", "div": "/", "and": "&", "or": "|", "xor": "^",

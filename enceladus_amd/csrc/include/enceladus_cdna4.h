@@ -33,11 +33,9 @@ EK_INLINE float bits_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
 EK_INLINE uint32_t f32_bits(float f) { return __builtin_bit_cast(uint32_t, f); }
 
 EK_INLINE float bf16_to_f32(bf16 h) { return bits_f32(((uint32_t)h.x) << 16); }
+// fp32 -> bf16, round to nearest even (gfx950 converts in hardware: v_cvt_pk_bf16_f32).
 EK_INLINE bf16 f32_to_bf16(float f) {
-  uint32_t u = f32_bits(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return bf16{(uint16_t)((u >> 16) | 0x40u)};  // quiet NaN
-  u += 0x7fffu + ((u >> 16) & 1u);  // round to nearest, ties to even
-  return bf16{(uint16_t)(u >> 16)};
+  return bf16{__builtin_bit_cast(uint16_t, (__bf16)f)};
 }
 
 // ---------------------------------------------------------------------------
@@ -154,6 +152,9 @@ template <typename T> EK_INLINE T ishr(T a, T b) {
   return (T)(a >> b);
 }
 EK_INLINE float fmodf_(float a, float b) { return __builtin_fmodf(a, b); }
+
+// 2^x with the hardware v_exp_f32 (1 ulp; results below 2^-126 flush to zero).
+EK_INLINE float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // ---------------------------------------------------------------------------
 // Raw vector moves. N is the byte count (1, 2, 4, 8 or 16).
