@@ -65,9 +65,12 @@ def make_launch(jfn, grid, args, num_warps=4, dot_warps=None, **constexprs):
         v = vals[n]
         packed.append(v.data_ptr() if hasattr(v, "data_ptr") else v)
     kern = lc.ck.pack(packed)
+    g, extra = lc.ck.launch_grid(grid)
+    if extra:
+        kern = kern + extra
+        kern += b"\0" * ((-len(kern)) % 8)
     buf = ctypes.create_string_buffer(kern, len(kern))
     fn = lc.ck.function()
-    g = (tuple(grid) + (1, 1, 1))[:3]
     blk = lc.ck.gen.block
     lib = hip.load_library()
     err = ctypes.create_string_buffer(256)

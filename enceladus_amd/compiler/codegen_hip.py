@@ -407,6 +407,10 @@ class Emitter:
         elif n in ("atomic_rmw", "atomic_cas"):
             self.kind[res.id] = "anchored"
             self.lay[res.id] = self.mem_layout(op.operands[0])
+            if res.id in getattr(self, "priv", {}):
+                idx = op.operands[0].op.operands[1]
+                if self._anch(idx) and self.lay[idx.id].shape == res.type.shape:
+                    self.lay[res.id] = self.lay[idx.id]
         elif n == "reshape":
             self.kind[res.id] = "anchored"
             self.lay[res.id] = self.default_layout(res)
@@ -665,6 +669,13 @@ class Emitter:
         conv = self.convert(src, sl)
         return f"{conv}[{ri}]"
 
+    def prime(self, *pairs):
+        """Materialises any conversion the given (value, layout) reads need, so that the
+        code for it is emitted before a loop header rather than inside the loop body."""
+        for v, lay in pairs:
+            if v is not None and self.tile(v):
+                self.elem(v, lay, "0")
+
     def array(self, v: ir.Value, lay: LY.Layout) -> str:
         """Name of an array holding `v` in exactly `lay` (materialising if needed)."""
         k = self.kind.get(v.id)
@@ -686,9 +697,10 @@ class Emitter:
                 return self.convert(src, sl)
         nm = self.fresh("m")
         t = ctype(v.type.dtype) + ("*" if v.type.ptr else "")
+        e = self.elem(v, lay, "r")
         self.emit(f"{t} {nm}[{lay.nregs}];")
         self.emit(f"#pragma unroll")
-        self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = {self.elem(v, lay, 'r')};")
+        self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = {e};")
         return nm
 
     # ------------------------------------------------------------------ LDS conversion
@@ -862,14 +874,15 @@ class Emitter:
     def op_program_id(self, op):
         nm = self.fresh("pid")
         ax = "xyz"[op.attrs["axis"]]
-        src = f"ek_pid_{ax}" if self.remap_pids else f"(int32_t)blockIdx.{ax}"
+        src = f"ek_pid_{ax}" if (self.remap_pids or self.coarsen) else \
+            f"(int32_t)blockIdx.{ax}"
         self.emit(f"const int32_t {nm} = {src};")
         self.define(op.result, nm)
 
     def op_num_programs(self, op):
         nm = self.fresh("np")
         ax = "xyz"[op.attrs["axis"]]
-        src = f"ek_np_{ax}" if self.opt.get("_coarsen") else f"(int32_t)gridDim.{ax}"
+        src = f"ek_np_{ax}" if self.coarsen else f"(int32_t)gridDim.{ax}"
         self.emit(f"const int32_t {nm} = {src};")
         self.define(op.result, nm)
 
@@ -893,6 +906,7 @@ class Emitter:
             return
         lay = self.lay[res.id]
         V = self.mem_vec(ptr, lay)
+        self.prime(*[(o, lay) for o in op.operands])
         nm = self.fresh("ld")
         self.emit(f"{t} {nm}[{lay.nregs}];")
         self.emit("#pragma unroll")
@@ -933,6 +947,7 @@ class Emitter:
                 lay = vl
         V = self.mem_vec(ptr, lay)
         own = self.owner_cond(lay)
+        self.prime((ptr, lay), (mask, lay))
         pe = lambda i: self.elem(ptr, lay, f"rv + {i}" if i else "rv")  # noqa: E731
         vals = self.array(val, lay)
         if own:
@@ -1047,6 +1062,77 @@ class Emitter:
             self.emit(f"  if ({cond}) {d['base']}[{addr}] = {vals}[rv];")
         self.emit("}")
 
+    # -- LDS-privatised histograms ----------------------------------------------------
+    def _and_terms(self, v: ir.Value, out: list):
+        op = v.op
+        if op is not None and op.name == "binary" and op.attrs["op"] == "and" and \
+                v.type.dtype.is_bool():
+            self._and_terms(op.operands[0], out)
+            self._and_terms(op.operands[1], out)
+        elif op is not None and op.name in ("broadcast", "expand_dims"):
+            self._and_terms(op.operands[0], out)
+        else:
+            out.append(v)
+
+    def _const_of(self, v: ir.Value):
+        while v.op is not None and v.op.name in ("splat", "broadcast", "expand_dims"):
+            v = v.op.operands[0]
+        if v.op is not None and v.op.name == "const":
+            return v.op.attrs["value"]
+        return None
+
+    def plan_privatization(self, fn: ir.Func):
+        """Finds `tl.atomic_add(base + idx, val, mask=... & (idx >= 0) & (idx < C))` on
+        32-bit integers with the result unused, `base` a kernel argument and C a constant
+        <= 16384: such bins live in LDS per workgroup and are flushed once at the end."""
+        self.priv: dict[int, dict] = {}
+        if self.opt.get("no_privatize"):
+            return
+        args = {a.id for a in fn.args}
+        for op in ir.walk(fn.body):
+            if op.name != "atomic_rmw" or op.attrs["op"] != "add" or not op.attrs.get("has_mask"):
+                continue
+            if self.uses.get(op.result.id) or not self.tile(op.result):
+                continue
+            dt = op.result.type.dtype
+            if dt not in (core.int32, core.uint32):
+                continue
+            ptr, val, mask = op.operands
+            p = ptr.op
+            if p is None or p.name != "ptr_add":
+                continue
+            base, idx = p.operands
+            while base.op is not None and base.op.name in ("splat", "broadcast"):
+                base = base.op.operands[0]
+            if base.id not in args:
+                continue
+            terms = []
+            self._and_terms(mask, terms)
+            lo_ok = hi = None
+            for t in terms:
+                o = t.op
+                if o is None or o.name != "binary":
+                    continue
+                a, b = o.operands
+                k = o.attrs["op"]
+                same = lambda x: x.id == idx.id  # noqa: E731
+                if k == "ge" and same(a) and self._const_of(b) == 0:
+                    lo_ok = True
+                elif k == "le" and same(b) and self._const_of(a) == 0:
+                    lo_ok = True
+                elif k == "lt" and same(a) and isinstance(self._const_of(b), int):
+                    hi = self._const_of(b)
+                elif k == "gt" and same(b) and isinstance(self._const_of(a), int):
+                    hi = self._const_of(a)
+            if lo_ok and hi is not None and 0 < hi <= 16384:
+                self.priv[op.result.id] = {"base": base, "bins": hi, "dt": dt}
+        if self.priv:
+            self.n_bins = max(i["bins"] for i in self.priv.values())
+            grids = {op.attrs["axis"] for op in ir.walk(fn.body)
+                     if op.name in ("program_id", "num_programs")}
+            self.coarsen = not self.opt.get("no_coarsen")
+            del grids
+
     # -- atomics --------------------------------------------------------------------
     def _atomic_call(self, kind: str, t: str, dt: core.dtype, p: str, v: str, cmp=None) -> str:
         scope = "__ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT"
@@ -1109,13 +1195,23 @@ class Emitter:
             return
         lay = self.lay[res.id]
         own = self.owner_cond(lay)
+        pv = self.priv.get(res.id) if hasattr(self, "priv") else None
+        if pv is not None:
+            idx = ptr.op.operands[1]
+            conds = [own] if own else []
+            conds.append(f"({self.elem(mask, lay, 'r')})")
+            ie = self.elem(idx, lay, "r")
+            ve = self.elem(val_v, lay, "r")
+            self.emit("#pragma unroll")
+            self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) if ({' && '.join(conds)}) "
+                      f"__hip_atomic_fetch_add(&ek_bins{pv['dt'].name}[{ie}], {ve}, "
+                      f"__ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);")
+            self.define(res, "ek_unused")
+            return
         if used and own:
             raise CompilationError("the result of a tl.atomic_* on a tile with replicated "
                                    "elements isn't supported; use a larger tile or fewer warps")
         nm = self.fresh("at")
-        self.emit(f"{t} {nm}[{lay.nregs}];")
-        self.emit("#pragma unroll")
-        self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {{")
         p = self.elem(ptr, lay, "r")
         v = self.elem(val_v, lay, "r")
         c = self.elem(cmp_v, lay, "r") if cmp_v is not None else None
@@ -1124,6 +1220,9 @@ class Emitter:
             conds.append(own)
         if mask is not None:
             conds.append(f"({self.elem(mask, lay, 'r')})")
+        self.emit(f"{t} {nm}[{lay.nregs}];")
+        self.emit("#pragma unroll")
+        self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {{")
         call = self._atomic_call(kind, t, dt, p, v, c)
         if conds:
             self.emit(f"  {nm}[r] = ({' && '.join(conds)}) ? {call} : ({t})0;")
@@ -1442,10 +1541,10 @@ class Emitter:
             nm = self.name[c.id]
         else:
             nm = self.fresh("acc")
+            e = self.elem(c, lc, "r")
             self.emit(f"float {nm}[{lc.nregs}];")
             self.emit("#pragma unroll")
-            self.emit(f"for (int r = 0; r < {lc.nregs}; ++r) {nm}[r] = "
-                      f"ek::f32({self.elem(c, lc, 'r')});")
+            self.emit(f"for (int r = 0; r < {lc.nregs}; ++r) {nm}[r] = ek::f32({e});")
         tm, tn, tk, kpl = plan.tm, plan.tn, plan.tk, ins.kpl
         # Per k step: read every A and B fragment first (staged operands come from LDS),
         # then issue the TM x TN MFMAs, so LDS latency overlaps the previous step's MFMAs.
@@ -1753,9 +1852,10 @@ class Emitter:
         lo, hi = (self.name[o.id] for o in op.operands[:2])
         lay = self.lay[acc_arg.id]
         nm = self.fresh("c")
+        e = self.elem(init, lay, "r")
         self.emit(f"float {nm}[{lay.nregs}];")
         self.emit("#pragma unroll")
-        self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = {self.elem(init, lay, 'r')};")
+        self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = {e};")
         self.emit("{")
         for o in g["scalar_ops"]:
             self.gen_op(o)
@@ -1792,10 +1892,10 @@ class Emitter:
                 self.emit(f"{t} {nm} = {self.name[i.id]};")
             else:
                 lay = self.lay[a.id]
+                e = self.elem(i, lay, "r")
                 self.emit(f"{t} {nm}[{lay.nregs}];")
                 self.emit("#pragma unroll")
-                self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = "
-                          f"{self.elem(i, lay, 'r')};")
+                self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = {e};")
         it = ctype(iv.type.dtype)
         ivn = self.fresh("iv")
         stg = self.stage_loops.get(id(op), []) if hasattr(self, "stage_loops") else []
@@ -1870,15 +1970,15 @@ class Emitter:
             if need_tmp:
                 tmp = self.fresh("y")
                 tt = ctype(t.type.dtype) + ("*" if t.type.ptr else "")
+                e = self.elem(v, lay, "r")
                 self.emit(f"{tt} {tmp}[{lay.nregs}];")
                 self.emit("#pragma unroll")
-                self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {tmp}[r] = "
-                          f"{self.elem(v, lay, 'r')};")
+                self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {tmp}[r] = {e};")
                 pend.append((nm, tmp, lay.nregs))
             else:
+                e = self.elem(v, lay, "r")
                 self.emit("#pragma unroll")
-                self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = "
-                          f"{self.elem(v, lay, 'r')};")
+                self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = {e};")
         for nm, tmp, n in pend:
             if n is None:
                 self.emit(f"{nm} = {tmp};")
@@ -1904,9 +2004,9 @@ class Emitter:
             for v, r, nm in zip(y.operands, op.results, names):
                 if self.tile(r):
                     lay = self.lay[r.id]
+                    e = self.elem(v, lay, "r")
                     self.emit("#pragma unroll")
-                    self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = "
-                              f"{self.elem(v, lay, 'r')};")
+                    self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = {e};")
                 else:
                     self.emit(f"{nm} = {self.name[v.id]};")
             self.pop_scope()
@@ -1938,10 +2038,15 @@ class Emitter:
             self.def_level[a.id] = 0
         self.plan_dots(fn)
         self.plan_staging(fn.body)
+        self.coarsen = False
+        self.plan_privatization(fn)
         self.assign_block(fn.body)
-        self.remap_pids = bool(self.dot_plans) and not self.opt.get("no_pid_remap")
+        self.remap_pids = bool(self.dot_plans) and not self.opt.get("no_pid_remap") and \
+            not self.coarsen
         self.gen_block(fn.body)
         kname = f"ek_{fn.name}"
+        if self.coarsen:
+            params += ["int32_t ek_np_x", "int32_t ek_np_y", "int32_t ek_np_z"]
         out = ['#include "enceladus_cdna4.h"', ""]
         attrs = f"__launch_bounds__({self.nt})"
         if getattr(self, "big_acc", 0) >= 128:
@@ -1981,9 +2086,43 @@ class Emitter:
                     yield from flat(it)
                 else:
                     yield it
-        out.extend(flat(self.scopes[0].items))
+        body = list(flat(self.scopes[0].items))
+        if self.priv:
+            dts = sorted({i["dt"].name for i in self.priv.values()})
+            for dn in dts:
+                out.append(f"  __shared__ {'int32_t' if dn == 'i32' else 'uint32_t'} "
+                           f"ek_bins{dn}[{self.n_bins}];")
+                out.append(f"  for (int i = ek_tid; i < {self.n_bins}; i += {self.nt}) "
+                           f"ek_bins{dn}[i] = 0;")
+            out.append("  __syncthreads();")
+        if self.coarsen:
+            # Program coarsening: a capped grid of workgroups walks the logical program ids
+            # (programs are independent; privatised atomics commute).
+            out.append("  const int ek_nprog = ek_np_x * ek_np_y * ek_np_z;")
+            out.append("  for (int ek_p = blockIdx.x; ek_p < ek_nprog; ek_p += gridDim.x) {")
+            out.append("  const int ek_pid_x = ek_p % ek_np_x;")
+            out.append("  const int ek_pid_y = (ek_p / ek_np_x) % ek_np_y;")
+            out.append("  const int ek_pid_z = ek_p / (ek_np_x * ek_np_y);")
+            out.append("  (void)ek_pid_x; (void)ek_pid_y; (void)ek_pid_z;")
+            out.extend(body)
+            out.append("  }")
+        else:
+            out.extend(body)
+        if self.priv:
+            out.append("  __syncthreads();")
+            for rid, info in self.priv.items():
+                dn = info["dt"].name
+                base = self.name[info["base"].id]
+                out.append(f"  for (int i = ek_tid; i < {info['bins']}; i += {self.nt}) {{")
+                out.append(f"    const auto v = ek_bins{dn}[i];")
+                out.append(f"    if (v) __hip_atomic_fetch_add({base} + i, v, __ATOMIC_RELAXED, "
+                           "__HIP_MEMORY_SCOPE_AGENT);")
+                out.append("  }")
+                break
         out.append("}")
-        return GeneratedKernel(kname, "\n".join(out) + "\n", args, self.nw, self.lds, self.nt)
+        gk = GeneratedKernel(kname, "\n".join(out) + "\n", args, self.nw, self.lds, self.nt)
+        gk.coarsen = 1 if self.coarsen else 0
+        return gk
 
 
 # Program-id remapping for kernels with tl.dot (programs are independent, so any bijection
@@ -2011,7 +2150,7 @@ def generate(fn: ir.Func, options: dict | None = None) -> GeneratedKernel:
     return Emitter(fn, options).run()
 
 
-def pack_args(kargs: list[KernelArg], values: list) -> bytes:
+def pack_args(kargs: list[KernelArg], values: list, pad8: bool = True) -> bytes:
     """Packs runtime argument values into the kernarg layout (natural alignment)."""
     buf = bytearray()
     for ka, v in zip(kargs, values):
@@ -2027,5 +2166,8 @@ def pack_args(kargs: list[KernelArg], values: list) -> bytes:
         pad = (-len(buf)) % size
         buf += b"\0" * pad
         buf += struct.pack("<" + fmt, v)
-    buf += b"\0" * ((-len(buf)) % 8)
+    if pad8:
+        buf += b"\0" * ((-len(buf)) % 8)
+    else:
+        buf += b"\0" * ((-len(buf)) % 4)
     return bytes(buf)

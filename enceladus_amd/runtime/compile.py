@@ -120,15 +120,45 @@ class CompiledKernel:
         return self._attrs
 
     def pack(self, values) -> bytes:
-        return codegen_hip.pack_args(self.args, values)
+        b = codegen_hip.pack_args(self.args, values, pad8=not self.gen.coarsen)
+        self.packed_size = len(b)
+        return b
+
+    def launch_grid(self, grid):
+        """(launch grid, extra kernarg bytes) for a logical program grid."""
+        gx, gy, gz = (tuple(grid) + (1, 1, 1))[:3]
+        if not self.gen.coarsen:
+            return (gx, gy, gz), b""
+        total = gx * gy * gz
+        cap = max(1, coarsen_cap())
+        import struct
+        return (min(total, cap), 1, 1), struct.pack("<iii", gx, gy, gz)
 
     def launch_raw(self, grid, kernarg: bytes, stream: int = 0):
         gx, gy, gz = (tuple(grid) + (1, 1, 1))[:3]
         if gx == 0 or gy == 0 or gz == 0:
             return
+        (gx, gy, gz), extra = self.launch_grid(grid)
+        if extra:
+            kernarg = kernarg[:self.packed_size] + extra
+            kernarg += b"\0" * ((-len(kernarg)) % 8)
         buf = ctypes.create_string_buffer(kernarg, len(kernarg))
         hip.call("ek_launch", ctypes.c_void_p(stream or None), self.function(), gx, gy, gz,
                  self.gen.block, 1, 1, 0, buf, len(kernarg))
+
+
+_CAP = None
+
+
+def coarsen_cap() -> int:
+    """Workgroups for coarsened kernels: 4 per compute unit of GPU 0."""
+    global _CAP
+    if _CAP is None:
+        try:
+            _CAP = 4 * hip.device_info(0).compute_units
+        except Exception:  # noqa: BLE001
+            _CAP = 1024
+    return _CAP
 
 
 def compile_ir(fn: ir.Func, options: dict | None = None) -> CompiledKernel:
