@@ -94,6 +94,21 @@ MATMUL_CONFIGS = [(256, 256, 64, 4), (256, 256, 32, 4), (256, 128, 64, 4), (128,
 ATTN_CONFIGS = [(128, 64, 4), (128, 128, 4), (128, 32, 4), (256, 64, 8), (256, 128, 8)]
 
 
+# num_warps swept for the HBM-bound row kernels (a launch option, as the autotuner would)
+HBM_WARPS = (4, 8, 16)
+
+
+def best_of(timer, steps, warmup, options, build):
+    best = None
+    for o in options:
+        ls = build(o)
+        ms = timer.run(ls, steps, warmup)
+        log(f"    num_warps={o}: {ms * 1e3:.1f} us")
+        if best is None or ms < best[0]:
+            best = (ms, ls, o)
+    return best
+
+
 def sets_for(bytes_per_set):
     return max(2, math.ceil(600e6 / bytes_per_set))
 
@@ -107,10 +122,10 @@ def w_softmax(torch, timer, steps, warmup):
     k = sets_for(nbytes)
     xs = [torch.randn(M, N, device="cuda", generator=None) for _ in range(k)]
     outs = [torch.empty_like(x) for x in xs]
-    launches = [make_launch(softmax_kernel, (M,), (o, x, N, N, N), BLOCK=8192)
-                for x, o in zip(xs, outs)]
-    ms = timer.run(launches, steps, warmup)
-    return {"name": "softmax", "config": "fp32 [4096, 8192]", "ms": ms,
+    ms, launches, nw = best_of(timer, steps, warmup, HBM_WARPS, lambda nw: [
+        make_launch(softmax_kernel, (M,), (o, x, N, N, N), BLOCK=8192, num_warps=nw)
+        for x, o in zip(xs, outs)])
+    return {"name": "softmax", "config": f"fp32 [4096, 8192] num_warps={nw}", "ms": ms,
             "bytes": nbytes, "gbps": nbytes / ms / 1e6, "bound": "hbm",
             "kernel": launches[0].ck.name}
 
@@ -124,10 +139,10 @@ def w_rmsnorm(torch, timer, steps, warmup):
     w = (torch.rand(N, generator=g) + 0.5).cuda()
     xs = [torch.randn(M, N, device="cuda") for _ in range(k)]
     outs = [torch.empty_like(x) for x in xs]
-    launches = [make_launch(rmsnorm_kernel, (M,), (x, w, o, N, N, N, 1e-6), BLOCK=8192)
-                for x, o in zip(xs, outs)]
-    ms = timer.run(launches, steps, warmup)
-    return {"name": "rmsnorm", "config": "fp32 [4096, 8192] eps 1e-6", "ms": ms,
+    ms, launches, nw = best_of(timer, steps, warmup, HBM_WARPS, lambda nw: [
+        make_launch(rmsnorm_kernel, (M,), (x, w, o, N, N, N, 1e-6), BLOCK=8192, num_warps=nw)
+        for x, o in zip(xs, outs)])
+    return {"name": "rmsnorm", "config": f"fp32 [4096, 8192] eps 1e-6 num_warps={nw}", "ms": ms,
             "bytes": nbytes, "gbps": nbytes / ms / 1e6, "bound": "hbm",
             "kernel": launches[0].ck.name}
 
@@ -203,11 +218,12 @@ def w_histogram(torch, timer, steps, warmup):
     g = torch.Generator(device="cpu").manual_seed(0)
     xs = [torch.randint(0, 1024, (n,), generator=g, dtype=torch.int32).cuda() for _ in range(3)]
     h = torch.zeros(1024, dtype=torch.int32, device="cuda")
-    launches = [make_launch(histogram_kernel, (n // 1024,), (x, h, n, 0.0, 1.0), NUM_BINS=1024,
-                            BLOCK=1024) for x in xs]
-    ms = timer.run(launches, max(4, steps // 4), 2)
+    ms, launches, nw = best_of(timer, max(4, steps // 4), 2, (4, 8), lambda nw: [
+        make_launch(histogram_kernel, (n // 1024,), (x, h, n, 0.0, 1.0), NUM_BINS=1024,
+                    BLOCK=1024, num_warps=nw) for x in xs])
     nbytes = 4 * n
-    return {"name": "histogram", "config": "int32 2^26 -> 1024 bins", "ms": ms, "bytes": nbytes,
+    return {"name": "histogram", "config": f"int32 2^26 -> 1024 bins num_warps={nw}", "ms": ms,
+            "bytes": nbytes,
             "gbps": nbytes / ms / 1e6, "bound": "hbm", "kernel": launches[0].ck.name}
 
 
@@ -219,10 +235,11 @@ def w_cumsum(torch, timer, steps, warmup):
     xs = [torch.randint(-100, 100, (M, N), generator=g, dtype=torch.int32).cuda()
           for _ in range(sets_for(nbytes))]
     outs = [torch.empty_like(x) for x in xs]
-    launches = [make_launch(cumsum_kernel, (M,), (o, x, M, N, N, N), REVERSE=False, BLOCK_M=1,
-                            BLOCK_N=4096) for x, o in zip(xs, outs)]
-    ms = timer.run(launches, steps, warmup)
-    return {"name": "cumsum", "config": "int32 [8192, 4096] rows", "ms": ms, "bytes": nbytes,
+    ms, launches, nw = best_of(timer, steps, warmup, HBM_WARPS, lambda nw: [
+        make_launch(cumsum_kernel, (M,), (o, x, M, N, N, N), REVERSE=False, BLOCK_M=1,
+                    BLOCK_N=4096, num_warps=nw) for x, o in zip(xs, outs)])
+    return {"name": "cumsum", "config": f"int32 [8192, 4096] rows num_warps={nw}", "ms": ms,
+            "bytes": nbytes,
             "gbps": nbytes / ms / 1e6, "bound": "hbm", "kernel": launches[0].ck.name}
 
 
@@ -239,6 +256,17 @@ def w_torch_matmul(torch, timer, steps, warmup):
             "kernel": "torch.matmul"}
 
 
+def w_copy_calib(torch, timer, steps, warmup):
+    """Calibration for HBM counters: a plain 256 MiB device-to-device copy."""
+    n = 64 << 20
+    x = torch.randn(n, device="cuda")
+    y = torch.empty_like(x)
+    ms = timer.run([lambda: y.copy_(x)], max(4, steps // 4), 2)
+    nbytes = 8 * n
+    return {"name": "copy_calib", "config": "torch copy 256 MiB -> 256 MiB", "ms": ms,
+            "bytes": nbytes, "gbps": nbytes / ms / 1e6, "bound": "hbm", "kernel": "copy"}
+
+
 WORKLOADS = {
     "softmax": w_softmax, "rmsnorm": w_rmsnorm, "vector_add": w_vector_add,
     "matmul": lambda t, tm, s, w: w_matmul(t, tm, s, w, False),
@@ -247,7 +275,21 @@ WORKLOADS = {
     "attention_noncausal": lambda t, tm, s, w: w_attention(t, tm, s, w, False, 1024),
     "histogram": w_histogram, "cumsum": w_cumsum,
     "torch_matmul": w_torch_matmul,
+    "copy_calib": w_copy_calib,
 }
+DEFAULT = [k for k in WORKLOADS if k not in ("torch_matmul", "copy_calib")]
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch for `kernel` from the committed rocprofv3 counter summary."""
+    import glob
+    for path in glob.glob(os.path.join(ROOT, "profiles", "*_hbm_counters.txt")):
+        text = open(path).read()
+        if kernel in text:
+            for line in text.splitlines():
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    return None
 
 
 def cpu_baseline(budget_s=12.0):
@@ -290,7 +332,7 @@ def main():
     info = hip.device_info(0)
     log(f"device: {info.name.decode()} {info.arch.decode()} CUs={info.compute_units}")
     timer = Timer(torch)
-    names = [n for n in (args.only.split(",") if args.only else WORKLOADS)]
+    names = args.only.split(",") if args.only else DEFAULT
     results = {}
     for n in names:
         log(f"[bench] {n} ...")
@@ -316,7 +358,8 @@ def main():
                    "cus": info.compute_units},
         "roofline": {"bound": head["bound"], "achieved": round(head.get("gbps", 0.0), 1),
                      "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": round(head["roofline_frac"], 4), "traffic": None},
+                     "frac": round(head["roofline_frac"], 4),
+                     "traffic": measured_traffic(head["kernel"])},
         "workloads": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
                           for kk, vv in v.items()} for k, v in results.items()},
     }

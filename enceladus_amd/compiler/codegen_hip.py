@@ -1128,10 +1128,7 @@ class Emitter:
                 self.priv[op.result.id] = {"base": base, "bins": hi, "dt": dt}
         if self.priv:
             self.n_bins = max(i["bins"] for i in self.priv.values())
-            grids = {op.attrs["axis"] for op in ir.walk(fn.body)
-                     if op.name in ("program_id", "num_programs")}
             self.coarsen = not self.opt.get("no_coarsen")
-            del grids
 
     # -- atomics --------------------------------------------------------------------
     def _atomic_call(self, kind: str, t: str, dt: core.dtype, p: str, v: str, cmp=None) -> str:
@@ -2038,7 +2035,7 @@ class Emitter:
             self.def_level[a.id] = 0
         self.plan_dots(fn)
         self.plan_staging(fn.body)
-        self.coarsen = False
+        self.coarsen = bool(self.opt.get("coarsen"))
         self.plan_privatization(fn)
         self.assign_block(fn.body)
         self.remap_pids = bool(self.dot_plans) and not self.opt.get("no_pid_remap") and \

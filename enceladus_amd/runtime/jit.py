@@ -230,6 +230,11 @@ class JITFunction:
 
     def _compile_for(self, types, facts, consts, num_warps, dot_warps) -> Launcher:
         options = {"dot_warps": tuple(dot_warps) if dot_warps else None}
+        # ENCELADUS_CODEGEN="flag,flag=value": emitter switches for experiments (e.g.
+        # no_staging, no_gemm_template, coarsen); part of the specialization key below.
+        for item in filter(None, os.environ.get("ENCELADUS_CODEGEN", "").split(",")):
+            k, _, v = item.partition("=")
+            options[k.strip()] = int(v) if v.strip().isdigit() else True
         fn_ir = C.build_module(self, types, facts, consts, num_warps, options)
         ck = C.compile_ir(fn_ir, options)
         runtime_names = list(types.keys())
@@ -237,7 +242,8 @@ class JITFunction:
 
     def _lookup(self, vals, num_warps, dot_warps) -> Launcher:
         types, facts, consts = self.specialize(vals)
-        key = self._key(types, facts, consts, num_warps, dot_warps)
+        key = (self._key(types, facts, consts, num_warps, dot_warps),
+               os.environ.get("ENCELADUS_CODEGEN", ""))
         lc = self._cache.get(key)
         if lc is None:
             lc = self._compile_for(types, facts, consts, num_warps, dot_warps)
