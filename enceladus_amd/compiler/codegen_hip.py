@@ -866,9 +866,24 @@ class Emitter:
         lay = self.lay[res.id]
         nm = self.fresh("t")
         xs = [self.elem(o, lay, "r") if self.tile(o) else self.name[o.id] for o in op.operands]
+        cond = None
+        if op.name == "select" and self.tile(op.operands[0]) and \
+                not self.opt.get("no_edge_versioning"):
+            cond = self.all_true(op.operands[0])
         self.emit(f"{t} {nm}[{lay.nregs}];")
-        self.emit("#pragma unroll")
-        self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = {self.ew(op, xs)};")
+        if cond:
+            # Edge versioning: a uniform branch skips the per-element mask when the whole
+            # tile is provably selected (interior blocks of a masked loop).
+            self.emit(f"if ({cond}) {{")
+            self.emit("  #pragma unroll")
+            self.emit(f"  for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = {xs[1]};")
+            self.emit("} else {")
+            self.emit("  #pragma unroll")
+            self.emit(f"  for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = {self.ew(op, xs)};")
+            self.emit("}")
+        else:
+            self.emit("#pragma unroll")
+            self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = {self.ew(op, xs)};")
         self.define(res, nm)
 
     def op_program_id(self, op):
@@ -1061,6 +1076,79 @@ class Emitter:
         else:
             self.emit(f"  if ({cond}) {d['base']}[{addr}] = {vals}[rv];")
         self.emit("}")
+
+    # -- interval analysis for edge versioning --------------------------------------------
+    def interval(self, v: ir.Value, depth=0):
+        """(lo, hi) C++ expressions bounding every element of an integer tile built from
+        aranges, splats, constants, + and -, and x constant; None when unknown."""
+        if depth > 32:
+            return None
+        k = self.kind.get(v.id)
+        if k == "scalar" and not isinstance(v.type, ir.DescType) and v.type.dtype.is_int() \
+                and not v.type.ptr and v.id in self.name:
+            nm = self.name[v.id]
+            return (nm, nm)
+        op = v.op
+        if op is None or v.type.ptr or not v.type.dtype.is_int() or v.type.dtype.is_bool():
+            return None
+        n = op.name
+        if n == "const":
+            x = str(int(op.attrs["value"]))
+            return (x, x)
+        if n == "arange":
+            st = op.attrs["start"]
+            return (str(st), str(st + v.type.shape[0] - 1))
+        if n in ("splat", "broadcast", "expand_dims", "hint"):
+            return self.interval(op.operands[0], depth + 1)
+        if n == "binary" and op.attrs["op"] in ("add", "sub", "mul"):
+            a = self.interval(op.operands[0], depth + 1)
+            b = self.interval(op.operands[1], depth + 1)
+            if a is None or b is None:
+                return None
+            kk = op.attrs["op"]
+            if kk == "add":
+                return (f"({a[0]} + {b[0]})", f"({a[1]} + {b[1]})")
+            if kk == "sub":
+                return (f"({a[0]} - {b[1]})", f"({a[1]} - {b[0]})")
+            for x, y in ((a, b), (b, a)):
+                if x[0] == x[1] and x[0].lstrip("-").isdigit() and int(x[0]) >= 0:
+                    return (f"({y[0]} * {x[0]})", f"({y[1]} * {x[0]})")
+            if a[0] == a[1] and b[0] == b[1]:
+                return (f"({a[0]} * {b[0]})", f"({a[0]} * {b[0]})")
+        return None
+
+    def all_true(self, m: ir.Value, depth=0):
+        """A uniform C++ condition under which every element of boolean tile `m` is true."""
+        if depth > 32 or m.op is None:
+            return None
+        op = m.op
+        n = op.name
+        if n in ("splat", "broadcast", "expand_dims"):
+            return self.all_true(op.operands[0], depth + 1)
+        if n == "const":
+            return "true" if op.attrs["value"] else None
+        if n != "binary":
+            return None
+        k = op.attrs["op"]
+        if k == "and":
+            a = self.all_true(op.operands[0], depth + 1)
+            b = self.all_true(op.operands[1], depth + 1)
+            return f"({a} && {b})" if a and b else None
+        if k not in ("lt", "le", "gt", "ge"):
+            return None
+        if op.operands[0].type.dtype.is_floating():
+            return None
+        a = self.interval(op.operands[0])
+        b = self.interval(op.operands[1])
+        if a is None or b is None:
+            return None
+        if k == "lt":
+            return f"({a[1]} < {b[0]})"
+        if k == "le":
+            return f"({a[1]} <= {b[0]})"
+        if k == "gt":
+            return f"({a[0]} > {b[1]})"
+        return f"({a[0]} >= {b[1]})"
 
     # -- LDS-privatised histograms ----------------------------------------------------
     def _and_terms(self, v: ir.Value, out: list):
@@ -1686,38 +1774,53 @@ class Emitter:
     def _stage_load(self, info, kval: str) -> list[str]:
         d = info["desc"]
         o0, o1 = self._stage_offsets(info, kval)
-        C, per, nvec = info["C"], info["per"], info["nvec"]
+        R, C, per, nvec = info["R"], info["C"], info["per"], info["nvec"]
         base, s0 = d["base"], d["strides"][0]
         sh0, sh1 = d["shape"][0], d["shape"][1]
         regs = info["regs"]
-        out = ["#pragma unroll", f"for (int i = 0; i < {per}; ++i) {{",
-               f"  const int c = ek_tid + i * {self.nt};"]
+        W = info.get("W", 8)
+        vt = "ek::u32x4" if (info["mode"] == "row" or W == 8) else "ek::u32x2"
+        head = ["#pragma unroll", f"for (int i = 0; i < {per}; ++i) {{",
+                f"  const int c = ek_tid + i * {self.nt};"]
         if nvec % self.nt:
-            out.append(f"  if (c >= {nvec}) break;")
+            head.append(f"  if (c >= {nvec}) break;")
         scalar = (f"(unsigned)gr < (unsigned){sh0} && (unsigned)(gc + e) < (unsigned){sh1}) ? "
                   f"reinterpret_cast<const uint16_t*>({base})[(int64_t)gr * {s0} + gc + e] : "
                   f"(uint16_t)0;")
+        # uniform interior test: the whole R x C block is inside the descriptor
+        full = (f"(({o0}) >= 0 && ({o0}) + {R} <= {sh0} && ({o1}) >= 0 && "
+                f"({o1}) + {C} <= {sh1})")
+        out = [f"if ({full}) {{"]
         if info["mode"] == "row":
-            out += [f"  const int r = c / {C // 8}, cc = (c % {C // 8}) * 8;",
-                    f"  const int gr = {o0} + r, gc = {o1} + cc;",
-                    f"  if ((unsigned)gr < (unsigned){sh0} && gc >= 0 && gc + 8 <= {sh1}) "
-                    f"{regs}[i] = *reinterpret_cast<const ek::u32x4*>({base} + (int64_t)gr * {s0} + gc);",
-                    "  else {", "    uint16_t h[8];",
-                    f"    for (int e = 0; e < 8; ++e) h[e] = ({scalar}",
-                    f"    __builtin_memcpy(&{regs}[i], h, 16);", "  }"]
+            out += ["  " + x for x in head] + [
+                f"    const int r = c / {C // 8}, cc = (c % {C // 8}) * 8;",
+                f"    {regs}[i] = *reinterpret_cast<const ek::u32x4*>({base} + (int64_t)({o0} + r)"
+                f" * {s0} + {o1} + cc);", "  }", "} else {"]
+            out += ["  " + x for x in head] + [
+                f"    const int r = c / {C // 8}, cc = (c % {C // 8}) * 8;",
+                f"    const int gr = {o0} + r, gc = {o1} + cc;",
+                f"    if ((unsigned)gr < (unsigned){sh0} && gc >= 0 && gc + 8 <= {sh1}) "
+                f"{regs}[i] = *reinterpret_cast<const ek::u32x4*>({base} + (int64_t)gr * {s0} + gc);",
+                "    else {", "      uint16_t h[8];",
+                f"      for (int e = 0; e < 8; ++e) h[e] = ({scalar}",
+                f"      __builtin_memcpy(&{regs}[i], h, 16);", "    }", "  }", "}"]
         else:
-            W = info["W"]
-            vt = "ek::u32x4" if W == 8 else "ek::u32x2"
-            out += [f"  const int rb = (c / {C // W}) * 8, cb = (c % {C // W}) * {W};",
-                    f"  const int gc = {o1} + cb;",
-                    "  #pragma unroll", "  for (int j = 0; j < 8; ++j) {",
-                    f"    const int gr = {o0} + rb + j;",
-                    f"    if ((unsigned)gr < (unsigned){sh0} && gc >= 0 && gc + {W} <= {sh1}) "
-                    f"{regs}[i * 8 + j] = *reinterpret_cast<const {vt}*>({base} + (int64_t)gr * {s0} + gc);",
-                    "    else {", f"      uint16_t h[{W}];",
-                    f"      for (int e = 0; e < {W}; ++e) h[e] = ({scalar}",
-                    f"      __builtin_memcpy(&{regs}[i * 8 + j], h, {2 * W});", "    }", "  }"]
-        out.append("}")
+            out += ["  " + x for x in head] + [
+                f"    const int rb = (c / {C // W}) * 8, cb = (c % {C // W}) * {W};",
+                "    #pragma unroll",
+                f"    for (int j = 0; j < 8; ++j) {regs}[i * 8 + j] = *reinterpret_cast<const {vt}*>"
+                f"({base} + (int64_t)({o0} + rb + j) * {s0} + {o1} + cb);", "  }", "} else {"]
+            out += ["  " + x for x in head] + [
+                f"    const int rb = (c / {C // W}) * 8, cb = (c % {C // W}) * {W};",
+                f"    const int gc = {o1} + cb;",
+                "    #pragma unroll", "    for (int j = 0; j < 8; ++j) {",
+                f"      const int gr = {o0} + rb + j;",
+                f"      if ((unsigned)gr < (unsigned){sh0} && gc >= 0 && gc + {W} <= {sh1}) "
+                f"{regs}[i * 8 + j] = *reinterpret_cast<const {vt}*>({base} + (int64_t)gr * {s0} + gc);",
+                "      else {", f"        uint16_t h[{W}];",
+                f"        for (int e = 0; e < {W}; ++e) h[e] = ({scalar}",
+                f"        __builtin_memcpy(&{regs}[i * 8 + j], h, {2 * W});", "      }", "    }",
+                "  }", "}"]
         return out
 
     def _stage_store(self, info, stage: str) -> list[str]:
