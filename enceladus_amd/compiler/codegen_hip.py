@@ -40,7 +40,7 @@ from enceladus_amd.language import core
 MAX_LDS = 160 * 1024
 
 _MATH = {"exp": "expf", "exp2": "ek::exp2_fast", "log": "logf", "log2": "log2f", "sqrt": "sqrtf",
-         "sin": "sinf", "cos": "cosf", "tanh": "tanhf", "erf": "erff", "floor": "floorf",
+         "sin": "sinf", "cos": "cosf", "tanh": "tanhf", "erf": "ek::erf_as", "floor": "floorf",
          "ceil": "ceilf"}
 _INFIX = {"add": "+", "sub": "-", "mul": "*", "div": "/", "and": "&", "or": "|", "xor": "^",
           "eq": "==", "ne": "!=", "lt": "<", "le": "<=", "gt": ">", "ge": ">="}
@@ -306,7 +306,7 @@ class Emitter:
         return lay
 
     def _anch(self, v):
-        return self.kind.get(v.id) in ("anchored", "view", "staged")
+        return self.kind.get(v.id) in ("anchored", "view", "staged", "fused")
 
     def assign_op(self, op: ir.Op):
         n = op.name
@@ -364,6 +364,8 @@ class Emitter:
                 self.kind[res.id] = "anchored"
                 pick = next((o for o in anch if self.kind[o.id] == "anchored"), anch[0])
                 self.lay[res.id] = self.lay[pick.id]
+                if self._fusable(op):
+                    self.kind[res.id] = "fused"
         elif n == "load":
             self.kind[res.id] = "anchored"
             lay = self.mem_layout(op.operands[0])
@@ -416,6 +418,28 @@ class Emitter:
             self.lay[res.id] = self.default_layout(res)
         else:
             raise CompilationError(f"the HIP backend doesn't lower `{n}`")
+
+    _EW_OPS = ("binary", "unary", "cast", "select", "fma", "bitcast")
+    _CHEAP_BIN = ("add", "sub", "mul", "and", "or", "xor", "min", "max", "eq", "ne", "lt",
+                  "le", "gt", "ge")
+
+    def _fusable(self, op: ir.Op) -> bool:
+        """Elementwise results consumed only by elementwise ops are emitted inline in their
+        consumers (no register array): single-use values always, multi-use ones when cheap."""
+        if self.opt.get("no_fusion"):
+            return False
+        us = self.uses.get(op.result.id, [])
+        if not us or any(u.name not in self._EW_OPS for u in us):
+            return False
+        if len(us) == 1:
+            return True
+        if op.name in ("cast", "select", "bitcast"):
+            return True
+        if op.name == "binary" and op.attrs["op"] in self._CHEAP_BIN:
+            return True
+        if op.name == "unary" and op.attrs["op"] in ("neg", "abs", "not"):
+            return True
+        return False
 
     def _use_layout(self, body: ir.Block, arg: ir.Value):
         """Layout of the first memory op that reads or writes through `arg`."""
@@ -653,11 +677,17 @@ class Emitter:
         k = self.kind.get(v.id)
         if k == "scalar":
             return self.name[v.id]
+        if k == "fused":
+            op = v.op
+            xs = [self.elem(o, lay, r) if self.tile(o) else self.name[o.id] for o in op.operands]
+            return self.ew(op, xs)
         if k == "cheap":
             return self.cheap(v, [self.coord(lay, d, r) for d in range(len(lay.shape))])
         src, sl, ri = self.resolve(v, lay, r)
         if self.kind.get(src.id) == "cheap":
             return self.cheap(src, [self.coord(sl, d, ri) for d in range(len(sl.shape))])
+        if self.kind.get(src.id) == "fused":
+            return self.elem(src, sl, ri)
         if self.kind.get(src.id) == "staged":
             return f"{self.read_staged(src, sl)}[{ri}]"
         a = self.lay[src.id]
@@ -860,7 +890,7 @@ class Emitter:
             self.emit(f"{t} const {nm} = {self.scalar_expr(op)};")
             self.define(res, nm)
             return
-        if k == "cheap":
+        if k in ("cheap", "fused"):
             self.def_level[res.id] = len(self.scopes) - 1
             return
         lay = self.lay[res.id]
@@ -2049,7 +2079,7 @@ class Emitter:
             s = v
             if self.kind.get(v.id) == "view":
                 s, _, _ = self.resolve(v, self.lay[v.id], "r")
-            if s.id in tids:
+            if s.id in tids or self.kind.get(s.id) == "fused":
                 need_tmp = True
         pend = []
         for v, t, nm in zip(vals, targets, names):

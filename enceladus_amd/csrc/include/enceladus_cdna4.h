@@ -153,6 +153,22 @@ template <typename T> EK_INLINE T ishr(T a, T b) {
 }
 EK_INLINE float fmodf_(float a, float b) { return __builtin_fmodf(a, b); }
 
+// erf(x) by Abramowitz & Stegun, Handbook of Mathematical Functions, formula 7.1.26:
+// erf(x) = 1 - (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-x^2), t = 1 / (1 + p x),
+// x >= 0, extended as an odd function; |error| <= 1.5e-7. Branch-free, so it unrolls well
+// in register-resident epilogues.
+EK_INLINE float erf_as(float x) {
+  const float ax = __builtin_fabsf(x);
+  const float t = 1.0f / __builtin_fmaf(0.3275911f, ax, 1.0f);
+  float poly = __builtin_fmaf(1.061405429f, t, -1.453152027f);
+  poly = __builtin_fmaf(poly, t, 1.421413741f);
+  poly = __builtin_fmaf(poly, t, -0.284496736f);
+  poly = __builtin_fmaf(poly, t, 0.254829592f);
+  poly *= t;
+  const float y = 1.0f - poly * __builtin_amdgcn_exp2f(-ax * ax * 1.4426950408889634f);
+  return __builtin_copysignf(y, x);
+}
+
 // 2^x with the hardware v_exp_f32 (1 ulp; results below 2^-126 flush to zero).
 EK_INLINE float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
