@@ -189,6 +189,18 @@ template <typename T, int V> EK_INLINE void vload(T* dst, const T* src) {
   R v = *reinterpret_cast<const R*>(src);
   __builtin_memcpy(dst, &v, sizeof(R));
 }
+// Streaming variants: non-temporal hint (data touched once; don't keep it in the caches).
+template <typename T, int V> EK_INLINE void vload_nt(T* dst, const T* src) {
+  typedef typename raw_t<sizeof(T) * V>::type R;
+  R v = __builtin_nontemporal_load(reinterpret_cast<const R*>(src));
+  __builtin_memcpy(dst, &v, sizeof(R));
+}
+template <typename T, int V> EK_INLINE void vstore_nt(T* dst, const T* src) {
+  typedef typename raw_t<sizeof(T) * V>::type R;
+  R v;
+  __builtin_memcpy(&v, src, sizeof(R));
+  __builtin_nontemporal_store(v, reinterpret_cast<R*>(dst));
+}
 template <typename T, int V> EK_INLINE void vstore(T* dst, const T* src) {
   typedef typename raw_t<sizeof(T) * V>::type R;
   R v;
