@@ -2011,7 +2011,11 @@ class Emitter:
         p = g["plan"]
         T = ctype(g["dt"])
         A, B = g["A"], g["B"]
-        tmpl = f"ek::Gemm<{T}, {g['bm']}, {g['bn']}, {g['bk']}, {p.wm}, {p.wn}, {self.nt}>"
+        # Buffer loads (hardware bounds checks) unless an operand may span >= 2 GiB.
+        big = any(v.facts.get("idx64") for v in (A["base_v"], B["base_v"]))
+        buf = "false" if big or self.opt.get("no_buffer_loads") else "true"
+        tmpl = (f"ek::Gemm<{T}, {g['bm']}, {g['bn']}, {g['bk']}, {p.wm}, {p.wn}, {self.nt}, "
+                f"{buf}>")
         self.need_lds(2 * (g["bm"] + g["bn"]) * g["bk"] * 2)
         self.emit(f"  {tmpl} ek_g;")
         self.emit(f"  ek_g.run({nm}, {A['base']}, {A['strides'][0]}, {B['base']}, "

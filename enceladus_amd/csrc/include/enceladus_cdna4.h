@@ -398,7 +398,19 @@ EK_INLINE void transpose8x4(const u32x2* r, u32x4* o) {
   }
 }
 
-template <typename T, int BM, int BN, int BK, int WM, int WN, int NT>
+// Raw buffer loads: the hardware range-checks each access against the resource size and
+// returns zeros out of range, so edge tiles need no per-element predicates. Offsets are in
+// bytes (< 2^31); a negative or too-large offset reads zeros.
+EK_INLINE __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t nbytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)nbytes,
+                                           0x00020000);
+}
+EK_INLINE u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
+constexpr int kOOB = 0x7ffffff0;  // an offset past any resource: loads read zeros
+
+template <typename T, int BM, int BN, int BK, int WM, int WN, int NT, bool BUF = false>
 struct Gemm {
   static constexpr int TM = BM / WM / 32, TN = BN / WN / 32, TK = BK / 16;
   static constexpr int KC = BK / 8;                    // 16-byte chunks per k row
@@ -418,6 +430,30 @@ struct Gemm {
 
   EK_INLINE void load(const uint16_t* A, int lda, const uint16_t* B, int ldb, int M, int N,
                       int K, int m0, int n0, int k, int tid) {
+    if constexpr (BUF) {
+      // Rows past M (A) or K (B) fall outside the resources; chunks past the last column
+      // are sent out of range explicitly.
+      const __amdgpu_buffer_rsrc_t ra_r = buffer_rsrc(A, (uint32_t)M * lda * 2);
+      const __amdgpu_buffer_rsrc_t rb_r = buffer_rsrc(B, (uint32_t)K * ldb * 2);
+#pragma unroll
+      for (int i = 0; i < A_CH; ++i) {
+        const int c = tid + i * NT, row = c / KC, kc = c % KC;
+        const int gk = k + kc * 8;
+        const int off = (gk + 8 <= K) ? ((m0 + row) * lda + gk) * 2 : kOOB;
+        ra[i] = buffer_load16(ra_r, off);
+      }
+#pragma unroll
+      for (int i = 0; i < B_BL; ++i) {
+        const int b = tid + i * NT, nb = b % (BN / 8), kb = b / (BN / 8);
+        if (B_TOTAL < NT && b >= B_TOTAL) break;
+        const int gn = n0 + nb * 8;
+        const int base = (gn + 8 <= N) ? ((k + kb * 8) * ldb + gn) * 2 : kOOB;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          rb[i][j] = buffer_load16(rb_r, base == kOOB ? kOOB : base + j * ldb * 2);
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < A_CH; ++i) {
       const int c = tid + i * NT, row = c / KC, kc = c % KC;

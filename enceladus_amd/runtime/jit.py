@@ -80,10 +80,24 @@ def arg_facts(value: Any) -> dict:
         return f
     if T.is_array_like(value):
         p = _data_ptr(value)
+        facts = {}
         if isinstance(value, np.ndarray):
-            return {"divisibility": 16}   # copied into a fresh 16-byte-aligned allocation
-        return {"divisibility": 16} if p is not None and p % 16 == 0 else {}
+            facts["divisibility"] = 16   # copied into a fresh 16-byte-aligned allocation
+        elif p is not None and p % 16 == 0:
+            facts["divisibility"] = 16
+        if _span_bytes(value) >= (1 << 31) - 64:
+            facts["idx64"] = True        # offsets may not fit 32-bit byte offsets
+        return facts
     return {}
+
+
+def _span_bytes(value) -> int:
+    shape = tuple(getattr(value, "shape", ()))
+    n = 1
+    for d in shape:
+        n *= int(d)
+    es = T.elem_dtype(value).itemsize
+    return n * es
 
 
 @dataclass(frozen=True)
