@@ -321,7 +321,14 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default="")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--mm", default="", help="only this matmul config: BM,BN,BK,num_warps")
+    ap.add_argument("--attn", default="", help="only this attention config: BM,BN,num_warps")
     args = ap.parse_args()
+    global MATMUL_CONFIGS, ATTN_CONFIGS
+    if args.mm:
+        MATMUL_CONFIGS = [tuple(int(x) for x in args.mm.split(","))]
+    if args.attn:
+        ATTN_CONFIGS = [tuple(int(x) for x in args.attn.split(","))]
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; multi-GPU runs are out "
                           "of scope (every config shards with no exchange; see DESIGN.md)"}))
