@@ -33,6 +33,7 @@ import numpy as np
 
 from enceladus_amd.compiler import ir
 from enceladus_amd.compiler import layout as LY
+from enceladus_amd.compiler import lds as LDS
 from enceladus_amd.compiler.axis_info import AxisAnalysis
 from enceladus_amd.compiler.errors import CompilationError
 from enceladus_amd.language import core
@@ -107,6 +108,9 @@ def bits_expr(r: str, pairs: list[tuple[int, int]]) -> str:
             t = f"({t} << {i})"
         terms.append(t)
     return " | ".join(terms) if len(terms) > 1 else terms[0]
+
+
+_STAGE_LAYOUTS: dict = {}
 
 
 @dataclass
@@ -1641,15 +1645,14 @@ class Emitter:
     def _frag_read(self, info, lay: LY.Layout, first: str, n: int, dst: str, decl=True):
         """Emits LDS reads of registers [first, first+n) of `lay` from a staged tile."""
         T = info["T"]
-        d, nb = lay.vec_dim_bits()
-        want = 1 if info["mode"] == "row" else 0
-        V = min(1 << nb, 8, n) if d == want else 1
+        lay_s = self._stage_view(info, lay)
+        d, nb = lay_s.vec_dim_bits()
+        V = min(1 << nb, 8, n) if d == info["pos_dim"] else 1
         sm = (f"(reinterpret_cast<const {T}*>({info['smem']}) + (ek_it{info['loop_idx']} & 1) * "
               f"{info['stage_elems']})")
         r = f"({first} + j)"
-        r0, r1 = self.coord(lay, 0, r), self.coord(lay, 1, r)
-        idx = f"({r0}) * {info['pitch']} + ({r1})" if info["mode"] == "row" else \
-            f"({r1}) * {info['pitch']} + ({r0})"
+        idx = info["sl"].cexpr(self.coord(lay_s, info["line_dim"], r),
+                               self.coord(lay_s, info["pos_dim"], r))
         if decl:
             self.emit(f"      {T} {dst}[{n}];")
         self.emit(f"    #pragma unroll")
@@ -1794,27 +1797,88 @@ class Emitter:
                 vals.append(self.name[o.id])
         return vals
 
+    @staticmethod
+    def _stage_view(info, lay: LY.Layout) -> LY.Layout:
+        """`lay` with the staged position dim's bits renamed to their storage bits."""
+        pd, sig = info["pos_dim"], info["sl"].sigma
+        return lay._map(lambda b: (pd, sig[b[1]]) if b[0] == pd else b, lay.shape)
+
+    def _stage_layout(self, info, W: int, nvec: int, per: int) -> LDS.StageLayout:
+        """Picks the LDS layout of a stage by simulating its stores and the dot's fragment
+        reads under the bank model of `lds.py`."""
+        R, C, lay = info["R"], info["C"], info["lay"]
+        row = info["mode"] == "row"
+        lines, length = (R, C) if row else (C, R)
+        pd, ld_ = (1, 0) if row else (0, 1)
+        if row:
+            sigma = LDS.identity_sigma(length)
+        else:
+            lead = []
+            for b in lay.reg:
+                if b[0] != 0 or len(lead) == 3:
+                    break
+                lead.append(b[1])
+            sigma = LDS.fragment_sigma(length, lead)
+        key = (info["mode"], R, C, W, self.nt, lay.key())
+        cache = _STAGE_LAYOUTS
+        if key in cache:
+            return cache[key][0]
+        acc = []
+        for w in range(self.nt // 64):
+            for i in range(per):
+                for q in range(1 if row else W):
+                    lanes = []
+                    for ln in range(64):
+                        c = w * 64 + ln + i * self.nt
+                        if c >= nvec:
+                            lanes.append(None)
+                        elif row:
+                            lanes.append((c // (C // 8), (c % (C // 8)) * 8))
+                        else:
+                            lanes.append(((c % (C // W)) * W + q, (c // (C // W)) * 8))
+                    acc.append((16, lanes))
+        probe = LDS.StageLayout(lines, length, length, sigma=sigma)
+        lay_s = self._stage_view({"pos_dim": pd, "sl": probe}, lay)
+        d, nb = lay_s.vec_dim_bits()
+        V = min(1 << nb, 8) if d == pd else 1
+        seen = set()
+        for w in range(lay_s.num_warps):
+            wc = lay_s.thread_coord(0, w)
+            if wc in seen:
+                continue
+            seen.add(wc)
+            for j in range(0, lay_s.nregs, V):
+                rc = lay_s.reg_coord(j)
+                lanes = []
+                for ln in range(64):
+                    tc = lay_s.thread_coord(ln, w)
+                    lanes.append((tc[ld_] | rc[ld_], tc[pd] | rc[pd]))
+                acc.append((2 * V, lanes))
+        sl, cyc = LDS.choose(lines, length, sigma, acc)
+        cache[key] = (sl, cyc, LDS.ideal(acc))
+        return sl
+
     def _stage_setup(self, info, idx: int):
         ld = info["op"]
         d = self.desc[ld.operands[0].id]
         R, C = info["R"], info["C"]
         T = ctype(ld.result.type.dtype)
         if info["mode"] == "row":
-            pitch = C + 8
-            stage_elems = R * pitch
+            W = 8
             nvec = R * C // 8
+            info.update({"line_dim": 0, "pos_dim": 1})
         else:
-            pitch = R + 8
-            stage_elems = C * pitch
             W = 8 if (R // 8) * (C // 8) >= self.nt or C % 4 else 4
-            info["W"] = W
             nvec = (R // 8) * (C // W)
+            info.update({"line_dim": 1, "pos_dim": 0})
+        info["W"] = W
         per = (nvec + self.nt - 1) // self.nt
+        sl = self._stage_layout(info, W, nvec, per)
         name = f"ek_stg{idx}"
-        info.update({"desc": d, "T": T, "pitch": pitch, "stage_elems": stage_elems,
+        info.update({"desc": d, "T": T, "sl": sl, "stage_elems": sl.elems,
                      "nvec": nvec, "per": per, "smem": name, "regs": f"ek_pf{idx}"})
-        self.extra_smem.append((name, 2 * stage_elems * 2))
-        if info["mode"] == "trans" and info["W"] == 4:
+        self.extra_smem.append((name, 2 * sl.elems * 2))
+        if info["mode"] == "trans" and W == 4:
             self.emit(f"ek::u32x2 {info['regs']}[{per * 8}];")
         else:
             regs = per * (8 if info["mode"] == "trans" else 1)
@@ -1854,16 +1918,22 @@ class Emitter:
                 f"      for (int e = 0; e < 8; ++e) h[e] = ({scalar}",
                 f"      __builtin_memcpy(&{regs}[i], h, 16);", "    }", "  }", "}"]
         else:
+            # storage positions rb..rb+7 hold logical rows rr + (the logical offset of j)
+            sig = info["sl"].sigma
+            rr = bits_expr("rb", [(s_, i_) for i_, s_ in enumerate(sig) if s_ >= 3])
+            rj = bits_expr("j", [(s_, i_) for i_, s_ in enumerate(sig) if s_ < 3])
+            idx_ = (f"    const int rb = (c / {C // W}) * 8, cb = (c % {C // W}) * {W}, "
+                    f"rr = {rr};")
             out += ["  " + x for x in head] + [
-                f"    const int rb = (c / {C // W}) * 8, cb = (c % {C // W}) * {W};",
+                idx_,
                 "    #pragma unroll",
                 f"    for (int j = 0; j < 8; ++j) {regs}[i * 8 + j] = *reinterpret_cast<const {vt}*>"
-                f"({base} + (int64_t)({o0} + rb + j) * {s0} + {o1} + cb);", "  }", "} else {"]
+                f"({base} + (int64_t)({o0} + rr + ({rj})) * {s0} + {o1} + cb);", "  }", "} else {"]
             out += ["  " + x for x in head] + [
-                f"    const int rb = (c / {C // W}) * 8, cb = (c % {C // W}) * {W};",
+                idx_,
                 f"    const int gc = {o1} + cb;",
                 "    #pragma unroll", "    for (int j = 0; j < 8; ++j) {",
-                f"      const int gr = {o0} + rb + j;",
+                f"      const int gr = {o0} + rr + ({rj});",
                 f"      if ((unsigned)gr < (unsigned){sh0} && gc >= 0 && gc + {W} <= {sh1}) "
                 f"{regs}[i * 8 + j] = *reinterpret_cast<const {vt}*>({base} + (int64_t)gr * {s0} + gc);",
                 "      else {", f"        uint16_t h[{W}];",
@@ -1874,7 +1944,7 @@ class Emitter:
 
     def _stage_store(self, info, stage: str) -> list[str]:
         C, per, nvec = info["C"], info["per"], info["nvec"]
-        regs, pitch = info["regs"], info["pitch"]
+        regs, sl = info["regs"], info["sl"]
         sm = f"(reinterpret_cast<uint16_t*>({info['smem']}) + ({stage}) * {info['stage_elems']})"
         out = ["#pragma unroll", f"for (int i = 0; i < {per}; ++i) {{",
                f"  const int c = ek_tid + i * {self.nt};"]
@@ -1882,7 +1952,7 @@ class Emitter:
             out.append(f"  if (c >= {nvec}) break;")
         if info["mode"] == "row":
             out += [f"  const int r = c / {C // 8}, cc = (c % {C // 8}) * 8;",
-                    f"  *reinterpret_cast<ek::u32x4*>({sm} + r * {pitch} + cc) = {regs}[i];"]
+                    f"  *reinterpret_cast<ek::u32x4*>({sm} + {sl.cexpr('r', 'cc')}) = {regs}[i];"]
         else:
             W = info["W"]
             out += [f"  const int rb = (c / {C // W}) * 8, cb = (c % {C // W}) * {W};",
@@ -1890,7 +1960,7 @@ class Emitter:
                     f"  ek::transpose8x{W}(&{regs}[i * 8], o);",
                     "  #pragma unroll",
                     f"  for (int q = 0; q < {W}; ++q) *reinterpret_cast<ek::u32x4*>({sm} + "
-                    f"(cb + q) * {pitch} + rb) = o[q];"]
+                    f"{sl.cexpr('cb + q', 'rb')}) = o[q];"]
         out.append("}")
         return out
 
@@ -1901,16 +1971,13 @@ class Emitter:
                 return sc.memo[key]
         info = self.staged[v.id]
         T = info["T"]
-        d, nb = lay.vec_dim_bits()
-        want = 1 if info["mode"] == "row" else 0
-        V = min(1 << nb, 8) if d == want else 1
+        lay_s = self._stage_view(info, lay)
+        d, nb = lay_s.vec_dim_bits()
+        V = min(1 << nb, 8) if d == info["pos_dim"] else 1
         sm = (f"(reinterpret_cast<const {T}*>({info['smem']}) + (ek_it{info['loop_idx']} & 1) * "
               f"{info['stage_elems']})")
-        r0, r1 = self.coord(lay, 0, "r"), self.coord(lay, 1, "r")
-        if info["mode"] == "row":
-            idx = f"({r0}) * {info['pitch']} + ({r1})"
-        else:
-            idx = f"({r1}) * {info['pitch']} + ({r0})"
+        idx = info["sl"].cexpr(self.coord(lay_s, info["line_dim"], "r"),
+                               self.coord(lay_s, info["pos_dim"], "r"))
         nm = self.fresh("sr")
         self.emit(f"{T} {nm}[{lay.nregs}];")
         self.emit("#pragma unroll")

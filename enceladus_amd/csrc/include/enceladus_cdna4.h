@@ -398,6 +398,20 @@ EK_INLINE void transpose8x4(const u32x2* r, u32x4* o) {
   }
 }
 
+// Element offset in a staged LDS tile. Lines of 2^LENSH elements are packed 2^LSH to a row of
+// PITCH elements; the 8-element chunk of a position inside its row is XOR-swizzled by
+// ((row >> SA) ^ (row >> SB)) & MASK.
+template <int PITCH, int MASK, int SA, int SB, int LSH, int LENSH>
+EK_INLINE int swz(int line, int sp) {
+  const int row = line >> LSH;
+  const int vp = ((line & ((1 << LSH) - 1)) << LENSH) | sp;
+  if constexpr (MASK == 0) {
+    return row * PITCH + vp;
+  } else {
+    return row * PITCH + (vp ^ ((((row >> SA) ^ (row >> SB)) & MASK) << 3));
+  }
+}
+
 // Raw buffer loads: the hardware range-checks each access against the resource size and
 // returns zeros out of range, so edge tiles need no per-element predicates. Offsets are in
 // bytes (< 2^31); a negative or too-large offset reads zeros.

@@ -113,8 +113,43 @@ def test_descriptor_dot_loop_uses_gemm_template():
     f16 = np.zeros(16, np.float16)
     src = codegen_hip.generate(matmul_desc_kernel.ir_for(
         f16, f16, f16, 4096, 4096, 4096, 4096, 4096, 4096, BM=256, BN=256, BK=64)).source
-    assert "ek::Gemm<_Float16, 256, 256, 64, 2, 2, 256>" in src
+    assert "ek::Gemm<_Float16, 256, 256, 64, 2, 2, 256, true>" in src
     # unaligned strides fall back to the generic lowering
     src2 = codegen_hip.generate(matmul_desc_kernel.ir_for(
         f16, f16, f16, 100, 90, 70, 70, 90, 90, BM=64, BN=64, BK=32)).source
     assert "ek::Gemm<" not in src2
+
+
+def test_lds_bank_model():
+    from enceladus_amd.compiler import lds
+    # 16-byte accesses to consecutive 16-byte slots: 8 lanes per pass, conflict-free
+    assert lds.pass_cycles([16 * i for i in range(64)], 16) == 8
+    # 8-byte accesses 128 bytes apart: the 16 lanes of a pass share one bank pair
+    assert lds.pass_cycles([128 * i for i in range(64)], 8) == 4 * 16
+    # one dword read by every lane is a broadcast: two 32-lane passes of one cycle
+    assert lds.pass_cycles([0] * 64, 4) == 2
+    # rows of 144 bytes read 8 bytes wide: rows r and r + 8 collide (2-way)
+    assert lds.pass_cycles([144 * (i % 32) + 8 * (i // 32) for i in range(64)], 8) == 8
+
+
+@pytest.mark.parametrize("head_dim,block_n", [(128, 64), (64, 64), (128, 32), (64, 128)])
+def test_attention_stage_layouts_are_bijective_and_conflict_free(head_dim, block_n):
+    import torch
+    from enceladus_amd.compiler import lds
+    from examples.flash_attention import attention_kernel
+    bf = torch.zeros(16, dtype=torch.bfloat16)
+    codegen_hip._STAGE_LAYOUTS.clear()
+    f = attention_kernel.ir_for(bf, bf, bf, bf, 0.088, 4096, 4096 * head_dim, head_dim,
+                                dot_warps=(4, 1), HEAD_DIM=head_dim, BLOCK_M=128,
+                                BLOCK_N=block_n, CAUSAL=True)
+    src = codegen_hip.generate(f, {"dot_warps": (4, 1)}).source
+    got = list(codegen_hip._STAGE_LAYOUTS.values())
+    assert len(got) == 2 and "ek::swz<" in src
+    for sl, cyc, ideal in got:
+        assert cyc == ideal, (sl, cyc, ideal)
+        assert [sl.logical(sl.sp(x)) for x in range(sl.length)] == list(range(sl.length))
+        offs = {sl.offset(ln, sl.sp(x)) for ln in range(sl.lines) for x in range(sl.length)}
+        assert len(offs) == sl.lines * sl.length and max(offs) < sl.elems
+        # a 16-byte chunk stays contiguous under the swizzle
+        assert all(sl.offset(ln, 8 * c + e) == sl.offset(ln, 8 * c) + e
+                   for ln in range(sl.lines) for c in range(sl.length // 8) for e in range(8))
