@@ -2078,9 +2078,12 @@ class Emitter:
         p = g["plan"]
         T = ctype(g["dt"])
         A, B = g["A"], g["B"]
-        # Buffer loads (hardware bounds checks) unless an operand may span >= 2 GiB.
+        # Buffer loads (hardware bounds checks) send a 16-byte chunk that is not wholly inside
+        # its row out of range, so they need K and N known to be multiples of 8; and no
+        # operand may span >= 2 GiB (32-bit byte offsets).
         big = any(v.facts.get("idx64") for v in (A["base_v"], B["base_v"]))
-        buf = "false" if big or self.opt.get("no_buffer_loads") else "true"
+        whole = all(self.axis.get(v).div[0] % 8 == 0 for v in (A["shape_v"][1], B["shape_v"][1]))
+        buf = "false" if big or not whole or self.opt.get("no_buffer_loads") else "true"
         tmpl = (f"ek::Gemm<{T}, {g['bm']}, {g['bn']}, {g['bk']}, {p.wm}, {p.wn}, {self.nt}, "
                 f"{buf}>")
         self.need_lds(2 * (g["bm"] + g["bn"]) * g["bk"] * 2)

@@ -472,13 +472,14 @@ struct Gemm {
     for (int i = 0; i < A_CH; ++i) {
       const int c = tid + i * NT, row = c / KC, kc = c % KC;
       const int gr = m0 + row, gk = k + kc * 8;
-      if (gr < M && gk + 8 <= K) {
+      if ((unsigned)gr < (unsigned)M && gk >= 0 && gk + 8 <= K) {
         ra[i] = *reinterpret_cast<const u32x4*>(A + (int64_t)gr * lda + gk);
       } else {
         uint16_t h[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-          h[e] = (gr < M && gk + e < K && gk + e >= 0) ? A[(int64_t)gr * lda + gk + e] : 0;
+          h[e] = ((unsigned)gr < (unsigned)M && (unsigned)(gk + e) < (unsigned)K)
+                     ? A[(int64_t)gr * lda + gk + e] : 0;
         __builtin_memcpy(&ra[i], h, 16);
       }
     }
@@ -490,13 +491,14 @@ struct Gemm {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int gk = k + kb * 8 + j;
-        if (gk < K && gn + 8 <= N) {
+        if ((unsigned)gk < (unsigned)K && gn >= 0 && gn + 8 <= N) {
           rb[i][j] = *reinterpret_cast<const u32x4*>(B + (int64_t)gk * ldb + gn);
         } else {
           uint16_t h[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e)
-            h[e] = (gk < K && gn + e < N) ? B[(int64_t)gk * ldb + gn + e] : 0;
+            h[e] = ((unsigned)gk < (unsigned)K && (unsigned)(gn + e) < (unsigned)N)
+                       ? B[(int64_t)gk * ldb + gn + e] : 0;
           __builtin_memcpy(&rb[i][j], h, 16);
         }
       }

@@ -5,6 +5,14 @@ and caches the code object under `$ENCELADUS_CACHE_DIR` (default
 `~/.cache/enceladus_amd`), keyed by the generated source, the compile options and the
 shim/header versions. Reference: src/enceladus/runtime/compile.py:38-164 and cache.py:26-144
 (disk cache of compiled kernels, corrupt entries recompiled).
+
+Environment variables (reference: src/enceladus/runtime/compile.py:6-10):
+    ENCELADUS_ALWAYS_COMPILE=1: ignore the disk cache.
+    ENCELADUS_DUMP=1: write the IR and HIP source of each new specialization next to the
+        cache and print their paths.
+    ENCELADUS_OVERRIDE_DIR: compile `<dir>/<kernel_name>.hip` instead of the generated
+        source when that file exists (it must define the same `ek_<kernel_name>` symbol
+        and take the same arguments).
 """
 
 from __future__ import annotations
@@ -13,6 +21,7 @@ import ctypes
 import hashlib
 import logging
 import os
+import sys
 import threading
 from pathlib import Path
 
@@ -163,8 +172,23 @@ def coarsen_cap() -> int:
 
 def compile_ir(fn: ir.Func, options: dict | None = None) -> CompiledKernel:
     gen = codegen_hip.generate(fn, options)
+    ir_text = ir.print_func(fn)
+    override = os.environ.get("ENCELADUS_OVERRIDE_DIR")
+    if override:
+        p = Path(override) / f"{fn.name}.hip"
+        if p.exists():
+            gen.source = p.read_text()
+            log.warning("enceladus: %s: compiling %s instead of the generated source", fn.name, p)
+    if os.environ.get("ENCELADUS_DUMP", "0") not in ("", "0"):
+        tag = hashlib.sha256(gen.source.encode()).hexdigest()[:12]
+        d = cache_dir() / "dump"
+        d.mkdir(parents=True, exist_ok=True)
+        (d / f"{fn.name}-{tag}.hip").write_text(gen.source)
+        (d / f"{fn.name}-{tag}.ir").write_text(ir_text)
+        print(f"enceladus: {fn.name}: IR and HIP source in {d}/{fn.name}-{tag}.{{ir,hip}}",
+              file=sys.stderr)
     code = compile_code(gen.source, gen.name)
-    return CompiledKernel(gen, ir.print_func(fn), code)
+    return CompiledKernel(gen, ir_text, code)
 
 
 def build_module(jfn, arg_types, arg_facts, constexprs, num_warps, options) -> ir.Func:

@@ -257,7 +257,8 @@ class JITFunction:
     def _lookup(self, vals, num_warps, dot_warps) -> Launcher:
         types, facts, consts = self.specialize(vals)
         key = (self._key(types, facts, consts, num_warps, dot_warps),
-               os.environ.get("ENCELADUS_CODEGEN", ""))
+               os.environ.get("ENCELADUS_CODEGEN", ""),
+               os.environ.get("ENCELADUS_OVERRIDE_DIR", ""))
         lc = self._cache.get(key)
         if lc is None:
             lc = self._compile_for(types, facts, consts, num_warps, dot_warps)

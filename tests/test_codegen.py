@@ -114,6 +114,10 @@ def test_descriptor_dot_loop_uses_gemm_template():
     src = codegen_hip.generate(matmul_desc_kernel.ir_for(
         f16, f16, f16, 4096, 4096, 4096, 4096, 4096, 4096, BM=256, BN=256, BK=64)).source
     assert "ek::Gemm<_Float16, 256, 256, 64, 2, 2, 256, true>" in src
+    # K and N not known to be multiples of 8: the template reads the row tails elementwise
+    src3 = codegen_hip.generate(matmul_desc_kernel.ir_for(
+        f16, f16, f16, 256, 250, 100, 112, 256, 250, BM=128, BN=128, BK=64)).source
+    assert "ek::Gemm<_Float16, 128, 128, 64, 2, 2, 256, false>" in src3
     # unaligned strides fall back to the generic lowering
     src2 = codegen_hip.generate(matmul_desc_kernel.ir_for(
         f16, f16, f16, 100, 90, 70, 70, 90, 90, BM=64, BN=64, BK=32)).source

@@ -9,6 +9,8 @@ add on both sides); float kernels use the tolerances stated in each test.
 import numpy as np
 import pytest
 
+import enceladus
+
 from oracle import interpreter as O
 from oracle import reference_np as R
 
@@ -173,6 +175,21 @@ def test_matmul_gemm_template(m, n, k, bm, bn, bk, nw):
     got = matmul_desc(a, b, bm=bm, bn=bn, bk=bk, num_warps=nw).astype(np.float32)
     want = R.matmul(a, b).astype(np.float32)
     np.testing.assert_allclose(got, want, rtol=2e-3, atol=1e-3)
+
+
+def test_matmul_template_row_tails():
+    """Row strides that are multiples of 16 elements around K and N that are not multiples of
+    8: the last partial 16-byte chunk of each row is read, not dropped."""
+    from examples.matmul import matmul_desc_kernel
+    m, n, k, kp, np_ = 256, 250, 100, 112, 256
+    _say(f"matmul template row tails {m}x{n}x{k} (row strides {kp}, {np_})")
+    a, b = _half((m, kp), 0, 1 / 8), _half((k, np_), 1, 1 / 8)
+    c = np.zeros((m, n), np.float16)
+    matmul_desc_kernel[(enceladus.cdiv(n, 128), enceladus.cdiv(m, 128))](
+        a, b, c, m, n, k, kp, np_, n, BM=128, BN=128, BK=64, num_warps=4)
+    want = R.matmul(np.ascontiguousarray(a[:, :k]), np.ascontiguousarray(b[:, :n]))
+    np.testing.assert_allclose(c.astype(np.float32), want.astype(np.float32), rtol=2e-3,
+                               atol=1e-3)
 
 
 def test_matmul_template_bf16_torch():
