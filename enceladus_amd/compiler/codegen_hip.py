@@ -1872,6 +1872,7 @@ class Emitter:
             nvec = (R // 8) * (C // W)
             info.update({"line_dim": 1, "pos_dim": 0})
         info["W"] = W
+        info["buf"] = self._stage_buffer_ok(info, d, W)
         per = (nvec + self.nt - 1) // self.nt
         sl = self._stage_layout(info, W, nvec, per)
         name = f"ek_stg{idx}"
@@ -1884,9 +1885,68 @@ class Emitter:
             regs = per * (8 if info["mode"] == "trans" else 1)
             self.emit(f"ek::u32x4 {info['regs']}[{regs}];")
 
+    def _stage_buffer_ok(self, info, d, W: int) -> bool:
+        """Whether a stage can load through raw buffer loads: 32-bit byte offsets, aligned
+        rows, and column chunks of W elements that lie wholly inside or outside the tile."""
+        if self.opt.get("no_buffer_loads") or d["base_v"].facts.get("idx64"):
+            return False
+        div = lambda v: self.axis.get(v).div[0]  # noqa: E731
+        if div(d["base_v"]) < 2 * W or div(d["stride_v"][0]) % W:
+            return False
+        if div(d["shape_v"][1]) % W:
+            return False
+        o1 = info["op"].operands[2]
+        return div(o1) % W == 0
+
+    def _stage_load_buffer(self, info, o0: str, o1: str) -> list[str]:
+        """Stage loads through one buffer resource: rows outside [0, shape0) fall past the
+        resource and read zeros in hardware, so there is no edge path. A tile that starts
+        far outside gets an empty resource, which also keeps the 32-bit offsets from
+        wrapping into range."""
+        d = info["desc"]
+        R, C, per, nvec = info["R"], info["C"], info["per"], info["nvec"]
+        base, s0 = d["base"], d["strides"][0]
+        sh0, sh1 = d["shape"][0], d["shape"][1]
+        regs, W = info["regs"], info["W"]
+        o1v = info["op"].operands[2]
+        o1c = int(o1v.op.attrs["value"]) if o1v.op is not None and o1v.op.name == "const" else None
+        sh1v = d["shape_v"][1]
+        sh1c = int(sh1v.op.attrs["value"]) if sh1v.op is not None and sh1v.op.name == "const" \
+            else None
+        cols_ok = o1c is not None and sh1c is not None and o1c >= 0 and o1c + C <= sh1c
+        out = ["{", f"  const int ek_r0 = {o0};",
+               f"  const __amdgpu_buffer_rsrc_t ek_rs = ek::buffer_rsrc({base}, "
+               f"(ek_r0 > -{R} && ek_r0 < {sh0}) ? (uint32_t){sh0} * (uint32_t){s0} * 2u : 0u);",
+               "  #pragma unroll", f"  for (int i = 0; i < {per}; ++i) {{",
+               f"    const int c = ek_tid + i * {self.nt};"]
+        if nvec % self.nt:
+            out.append(f"    if (c >= {nvec}) break;")
+        if info["mode"] == "row":
+            chk = "" if cols_ok else f"(gc >= 0 && gc + 8 <= {sh1}) ? "
+            tail = "" if cols_ok else " : ek::kOOB"
+            out += [f"    const int r = c / {C // 8}, cc = (c % {C // 8}) * 8, gc = {o1} + cc;",
+                    f"    {regs}[i] = ek::buffer_load16(ek_rs, {chk}((ek_r0 + r) * {s0} + gc) * 2"
+                    f"{tail});"]
+        else:
+            sig = info["sl"].sigma
+            rr = bits_expr("rb", [(s_, i_) for i_, s_ in enumerate(sig) if s_ >= 3])
+            rj = bits_expr("j", [(s_, i_) for i_, s_ in enumerate(sig) if s_ < 3])
+            ld = "buffer_load16" if W == 8 else "buffer_load8"
+            chk = "" if cols_ok else f"(gc >= 0 && gc + {W} <= {sh1}) ? "
+            tail = "" if cols_ok else " : ek::kOOB"
+            out += [f"    const int rb = (c / {C // W}) * 8, cb = (c % {C // W}) * {W}, "
+                    f"rr = {rr}, gc = {o1} + cb;",
+                    "    #pragma unroll",
+                    f"    for (int j = 0; j < 8; ++j) {regs}[i * 8 + j] = ek::{ld}(ek_rs, "
+                    f"{chk}((ek_r0 + rr + ({rj})) * {s0} + gc) * 2{tail});"]
+        out += ["  }", "}"]
+        return out
+
     def _stage_load(self, info, kval: str) -> list[str]:
         d = info["desc"]
         o0, o1 = self._stage_offsets(info, kval)
+        if info.get("buf"):
+            return self._stage_load_buffer(info, o0, o1)
         R, C, per, nvec = info["R"], info["C"], info["per"], info["nvec"]
         base, s0 = d["base"], d["strides"][0]
         sh0, sh1 = d["shape"][0], d["shape"][1]
@@ -2137,6 +2197,10 @@ class Emitter:
                     self.emit("  " + ln)
             self.emit("}")
             self.emit("__syncthreads();")
+            # s_waitcnt vmcnt(0): no global load is outstanding at the loop head on any path,
+            # so the first use of a register loaded before the loop does not also wait for
+            # the next tile's prefetch issued at the top of the body.
+            self.emit("__builtin_amdgcn_s_waitcnt(0x0F70);")
         self.push_scope(f"for ({it} {ivn} = {lo}; {ivn} < {hi}; {ivn} += {step}) {{")
         self.define(iv, ivn)
         for a, nm in zip(carried, names):

@@ -422,6 +422,9 @@ EK_INLINE __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t nbytes) 
 EK_INLINE u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int byte_off) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
 }
+EK_INLINE u32x2 buffer_load8(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, 0));
+}
 constexpr int kOOB = 0x7ffffff0;  // an offset past any resource: loads read zeros
 
 template <typename T, int BM, int BN, int BK, int WM, int WN, int NT, bool BUF = false>
@@ -571,6 +574,9 @@ struct Gemm {
     load(A16, lda, B16, ldb, M, N, K, m0, n0, lo, tid);
     store(s16, tid);
     __syncthreads();
+    // s_waitcnt vmcnt(0): nothing loaded before the loop (the accumulator's initial value
+    // included) is outstanding at its head, so the first MFMA does not wait for the prefetch.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
     for (int it = 0; it < niter; ++it) {
       const bool more = it + 1 < niter;
       if (more) load(A16, lda, B16, ldb, M, N, K, m0, n0, lo + (it + 1) * BK, tid);
