@@ -87,7 +87,7 @@ def make_launch(jfn, grid, args, num_warps=4, dot_warps=None, **constexprs):
 
 # (BM, BN, BK, num_warps) swept for the matmul rows: the autotuner's MI355X candidates
 MATMUL_CONFIGS = [(256, 256, 64, 4), (256, 256, 32, 4), (256, 128, 64, 4), (128, 256, 64, 4),
-                  (128, 128, 64, 4), (256, 256, 64, 8)]
+                  (128, 128, 64, 4), (256, 256, 64, 8), (256, 256, 32, 8)]
 
 
 # (BLOCK_M, BLOCK_N, num_warps) swept for the attention rows (dot_warps = (num_warps, 1))

@@ -1836,7 +1836,7 @@ class Emitter:
                             lanes.append((c // (C // 8), (c % (C // 8)) * 8))
                         else:
                             lanes.append(((c % (C // W)) * W + q, (c // (C // W)) * 8))
-                    acc.append((16, lanes))
+                    acc.append((16, lanes, True))
         probe = LDS.StageLayout(lines, length, length, sigma=sigma)
         lay_s = self._stage_view({"pos_dim": pd, "sl": probe}, lay)
         d, nb = lay_s.vec_dim_bits()
@@ -1853,7 +1853,7 @@ class Emitter:
                 for ln in range(64):
                     tc = lay_s.thread_coord(ln, w)
                     lanes.append((tc[ld_] | rc[ld_], tc[pd] | rc[pd]))
-                acc.append((2 * V, lanes))
+                acc.append((2 * V, lanes, False))
         sl, cyc = LDS.choose(lines, length, sigma, acc)
         cache[key] = (sl, cyc, LDS.ideal(acc))
         return sl
@@ -2143,10 +2143,25 @@ class Emitter:
         # operand may span >= 2 GiB (32-bit byte offsets).
         big = any(v.facts.get("idx64") for v in (A["base_v"], B["base_v"]))
         whole = all(self.axis.get(v).div[0] % 8 == 0 for v in (A["shape_v"][1], B["shape_v"][1]))
-        buf = "false" if big or not whole or self.opt.get("no_buffer_loads") else "true"
-        tmpl = (f"ek::Gemm<{T}, {g['bm']}, {g['bn']}, {g['bk']}, {p.wm}, {p.wn}, {self.nt}, "
-                f"{buf}>")
-        self.need_lds(2 * (g["bm"] + g["bn"]) * g["bk"] * 2)
+        buf = not (big or not whole or self.opt.get("no_buffer_loads"))
+        bm, bn, bk = g["bm"], g["bn"], g["bk"]
+        stage = (bm * bk + bk * bn) * 2
+        dma = (buf and not self.opt.get("no_lds_dma") and (bm * bk // 8) % self.nt == 0
+               and (bk * bn // 8) % self.nt == 0 and bn >= 32)
+        if dma:
+            # Stages: as many (at most 4) as fit the LDS share of a workgroup when a CU keeps
+            # 8 waves (2 per SIMD) resident; or the `gemm_stages` option.
+            share = 163840 // max(1, 8 // (self.nt // 64))
+            nst = int(self.opt.get("gemm_stages", 0)) or max(2, min(4, share // stage))
+            d = (bm * bk // 8 + bk * bn // 8) // self.nt
+            while nst > 2 and ((nst - 2) * d > 63 or nst * stage > 163840):
+                nst -= 1
+            tmpl = f"ek::GemmDma<{T}, {bm}, {bn}, {bk}, {p.wm}, {p.wn}, {self.nt}, {nst}>"
+            self.need_lds(nst * stage)
+        else:
+            tmpl = (f"ek::Gemm<{T}, {bm}, {bn}, {bk}, {p.wm}, {p.wn}, {self.nt}, "
+                    f"{'true' if buf else 'false'}>")
+            self.need_lds(2 * stage)
         self.emit(f"  {tmpl} ek_g;")
         self.emit(f"  ek_g.run({nm}, {A['base']}, {A['strides'][0]}, {B['base']}, "
                   f"{B['strides'][0]}, {A['shape'][0]}, {B['shape'][1]}, {A['shape'][1]}, "

@@ -11,18 +11,21 @@ index inside a row is then XOR-swizzled by a function of the row:
     offset(line, sp) = row * pitch + (vp ^ (h(row) << 3)),
     h(row) = ((row >> sa) ^ (row >> sb)) & mask
 
-Bank model (CDNA LDS): 32 banks of 4 bytes. A wave's access of `w` bytes per lane is served
-`128 / w` consecutive lanes per pass; a pass takes as many cycles as the largest number of
-distinct dwords that fall on one bank (lanes reading the same dword share it). The chooser
-simulates every store the stage loader issues and every fragment read the dot issues and
-keeps the cheapest candidate; ties go to no swizzle, then to the smaller pitch.
+Bank model (gfx950 LDS, measured with SQ_LDS_BANK_CONFLICT on access-pattern kernels): a
+read is served 256 bytes per cycle (64 banks of 4 bytes): 16 lanes per pass for 16-byte
+reads, 32 lanes for 8-byte reads. A write is served 128 bytes per cycle: 8 lanes per pass
+for 16-byte writes. A pass takes as many cycles as the largest number of distinct dwords
+that fall on one bank (lanes reading the same dword share it). The chooser simulates every
+store the stage loader issues and every fragment read the dot issues and keeps the
+cheapest candidate; ties go to no swizzle, then to the smaller pitch.
 """
 
 from __future__ import annotations
 
 from dataclasses import dataclass
 
-BANKS = 32
+READ_BYTES = 256    # bytes per read pass (64 banks)
+WRITE_BYTES = 128   # bytes per write pass
 BANK_BYTES = 4
 NO_SHIFT = 31  # `line >> 31` is 0 for every line index, so (a, 31) is a single-shift hash
 
@@ -36,11 +39,12 @@ class StageLayout:
     sa: int = 0
     sb: int = NO_SHIFT
     sigma: tuple = ()    # sigma[i] = storage bit of logical position bit i
+    rowlen: int = 64     # lines shorter than this are packed to rows of `rowlen` elements
 
     @property
     def k(self) -> int:
         """Lines per row."""
-        return max(1, 64 // self.length)
+        return max(1, self.rowlen // self.length)
 
     @property
     def rows(self) -> int:
@@ -75,7 +79,7 @@ class StageLayout:
 
     def cexpr(self, line: str, sp: str) -> str:
         """C++ element offset for the line and storage-position expressions."""
-        lsh = self.k.bit_length() - 1
+        lsh = self.k.bit_length() - 1  # lines per row = 2^lsh
         lensh = self.length.bit_length() - 1
         return (f"ek::swz<{self.pitch}, {self.mask}, {self.sa}, {self.sb}, {lsh}, {lensh}>"
                 f"({line}, {sp})")
@@ -98,9 +102,11 @@ def fragment_sigma(length: int, lead: list[int]) -> tuple:
     return tuple(sigma)
 
 
-def pass_cycles(addrs: list, width: int) -> int:
+def pass_cycles(addrs: list, width: int, write: bool = False) -> int:
     """Cycles of one wave access: `addrs` holds 64 byte addresses (None = inactive lane)."""
-    group = (BANKS * BANK_BYTES) // width
+    span = WRITE_BYTES if write else READ_BYTES
+    group = span // width
+    banks_n = span // BANK_BYTES
     total = 0
     for g0 in range(0, len(addrs), group):
         banks: dict[int, set] = {}
@@ -109,40 +115,44 @@ def pass_cycles(addrs: list, width: int) -> int:
                 continue
             for w in range(width // BANK_BYTES):
                 dw = a // BANK_BYTES + w
-                banks.setdefault(dw % BANKS, set()).add(dw)
+                banks.setdefault(dw % banks_n, set()).add(dw)
         if banks:
             total += max(len(s) for s in banks.values())
     return total
 
 
 def cost(lay: StageLayout, accesses: list) -> int:
-    """Total cycles of `accesses`: (width_bytes, [(line, sp) | None] * 64) tuples."""
+    """Total cycles of `accesses`: (width_bytes, [(line, sp) | None] * 64, is_write)."""
     tot = 0
-    for width, lanes in accesses:
+    for width, lanes, write in accesses:
         addrs = [None if x is None else 2 * lay.offset(*x) for x in lanes]
-        tot += pass_cycles(addrs, width)
+        tot += pass_cycles(addrs, width, write)
     return tot
 
 
 def ideal(accesses: list) -> int:
     """Cycles of `accesses` with no bank conflict: one per pass."""
     tot = 0
-    for w, lanes in accesses:
-        g = (BANKS * BANK_BYTES) // w
+    for w, lanes, write in accesses:
+        g = (WRITE_BYTES if write else READ_BYTES) // w
         tot += sum(1 for g0 in range(0, len(lanes), g) if any(x is not None for x in lanes[g0:g0 + g]))
     return tot
 
 
 def candidates(lines: int, length: int, sigma: tuple) -> list[StageLayout]:
-    rowlen = max(length, 64)
-    out = [StageLayout(lines, length, rowlen + 8, sigma=sigma),
-           StageLayout(lines, length, rowlen, sigma=sigma)]
-    m = min(rowlen // 8, 8) - 1
-    for a in range(5):
-        out.append(StageLayout(lines, length, rowlen, m, a, NO_SHIFT, sigma))
-    for a in range(4):
-        for b in range(a + 1, 7):
-            out.append(StageLayout(lines, length, rowlen, m, a, b, sigma))
+    out = []
+    for rl in (64, 128):
+        rowlen = max(length, rl)
+        if out and rowlen == out[0].rowlen:
+            continue
+        out += [StageLayout(lines, length, rowlen + 8, sigma=sigma, rowlen=rowlen),
+                StageLayout(lines, length, rowlen, sigma=sigma, rowlen=rowlen)]
+        m = min(rowlen // 8, 16) - 1
+        for a in range(5):
+            out.append(StageLayout(lines, length, rowlen, m, a, NO_SHIFT, sigma, rowlen))
+        for a in range(4):
+            for b in range(a + 1, 7):
+                out.append(StageLayout(lines, length, rowlen, m, a, b, sigma, rowlen))
     return out
 
 

@@ -427,11 +427,28 @@ EK_INLINE u32x2 buffer_load8(__amdgpu_buffer_rsrc_t r, int byte_off) {
 }
 constexpr int kOOB = 0x7ffffff0;  // an offset past any resource: loads read zeros
 
+// Buffer resource as four SGPR words, for the inline-asm copy below.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+EK_INLINE i32x4 rsrc_words(const void* base, uint32_t nbytes) {
+  const uint64_t b = (uint64_t)base;
+  return i32x4{(int)(uint32_t)b, (int)((b >> 32) & 0xffff), (int)nbytes, 0x00020000};
+}
+// LDS byte address of a pointer into __shared__ memory.
+EK_INLINE uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uint64_t)(const __attribute__((address_space(3))) void*)p;
+}
+// One 16-byte-per-lane global -> LDS copy (buffer_load_dwordx4 ... lds): lane l's chunk lands
+// at LDS byte `lds + 16 * l` (`lds` is wave-uniform). Issued from inline asm so the compiler
+// does not order later LDS reads behind it: the caller waits with an explicit vmcnt.
+EK_INLINE void dma16(i32x4 rsrc, uint32_t lds, int voff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               ::"s"(lds), "v"(voff), "s"(rsrc) : "memory", "m0");
+}
+
 template <typename T, int BM, int BN, int BK, int WM, int WN, int NT, bool BUF = false>
 struct Gemm {
   static constexpr int TM = BM / WM / 32, TN = BN / WN / 32, TK = BK / 16;
   static constexpr int KC = BK / 8;                    // 16-byte chunks per k row
-  static constexpr int SWZ = (KC < 8 ? KC : 8) - 1;    // xor mask for the chunk index
   static constexpr int A_CH = BM * KC / NT;            // A chunks per thread
   static constexpr int B_TOTAL = KC * (BN / 8);        // B 8x8 blocks per tile
   static constexpr int B_BL = (B_TOTAL + NT - 1) / NT; // B 8x8 blocks per thread
@@ -508,13 +525,17 @@ struct Gemm {
     }
   }
 
-  // LDS addressing (in 16-byte chunks). A: row-major [BM][KC] chunks, chunk index xor'ed
-  // with (row >> 1) & 7, so 16 consecutive rows (reads) and 8 chunks x 2 rows (writes)
-  // each cover all 64 banks. B^T: k-chunk-major [KC][BN] chunks with the column
-  // permuted as n ^ ((n >> 4) & 7), so reads of 16 consecutive columns and writes of
-  // columns 8 apart (one per 8x8 block) are both conflict-free.
-  static EK_INLINE int a_chunk(int row, int kc) { return row * KC + (kc ^ ((row >> 1) & SWZ)); }
-  static EK_INLINE int b_chunk(int n, int kc) { return kc * BN + (n ^ ((n >> 4) & 7)); }
+  // LDS addressing (in 16-byte chunks). gfx950 serves LDS reads 256 bytes per pass (16
+  // lanes of 16 bytes) and writes 128 bytes per pass (8 lanes). A: row-major [BM][KC]
+  // chunks, chunk index xor'ed with (row >> ASH) & AMASK, so the 16 rows a read pass
+  // touches land on 16 distinct chunk slots and a write pass (8 chunks of one row) stays
+  // contiguous. B^T: k-chunk-major [KC][BN] chunks with the column permuted as
+  // n ^ ((n >> 3) & 7), so reads of 16 consecutive columns and writes of the 8 columns
+  // n = 8 nb + q (one per 8x8 block) are both conflict-free.
+  static constexpr int ASH = KC >= 16 ? 0 : (KC == 8 ? 1 : (KC == 4 ? 2 : 3));
+  static constexpr int AMASK = (KC < 16 ? KC : 16) - 1;
+  static EK_INLINE int a_chunk(int row, int kc) { return row * KC + (kc ^ ((row >> ASH) & AMASK)); }
+  static EK_INLINE int b_chunk(int n, int kc) { return kc * BN + (n ^ ((n >> 3) & 7)); }
 
   EK_INLINE void store(uint16_t* st, int tid) {
     u32x4* sA = reinterpret_cast<u32x4*>(st);
@@ -584,6 +605,150 @@ struct Gemm {
       if (more) store(s16 + ((it + 1) & 1) * STAGE, tid);
       __syncthreads();
     }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// GEMM main loop fed by LDS DMA: C[BM x BN] += A[BM x K] * B[K x BN], 16-bit row-major
+// operands, fp32 accumulators in the 32x32x16 MFMA layout (same as Gemm).
+//
+//  - Tiles move global -> LDS with buffer_load ... lds (16 bytes per lane, no VGPRs): the 64
+//    lanes of one instruction fill 64 consecutive 16-byte LDS chunks, so each lane fetches
+//    the global chunk that belongs at its LDS position under the swizzle below. Rows past
+//    M (A) or K (B) fall outside the buffer resource and arrive as zeros; chunks past the
+//    last column are sent out of range explicitly (K and N are multiples of 8).
+//  - S stages in LDS; S - 1 tiles are in flight while one is computed. A stage is waited
+//    for with an explicit vmcnt (this wave's copies) and a barrier (everyone's), which also
+//    frees the stage consumed one step earlier for the next copy.
+//  - A fragments are 16-byte LDS reads; B stays row-major in LDS and its k-major fragments
+//    come from ds_read_b64_tr_b16: in each group of 16 lanes, lane 4i + q reads 4 columns of
+//    k row i, and output lane L receives column L of the 4 rows.
+//  - LDS swizzles (reads are served 256 bytes per pass): A chunk (row, kc) sits at
+//    row * KC + (kc ^ ((row >> ASH) & AMASK)); B chunk (k, nc) at
+//    k * NCB + (nc ^ (((k >> RSH) & RMASK) << 2)), which spreads the 4 rows a transpose
+//    read touches over the 4 64-byte quarters of a pass.
+// ---------------------------------------------------------------------------
+template <typename T, int BM, int BN, int BK, int WM, int WN, int NT, int S>
+struct GemmDma {
+  static constexpr int TM = BM / WM / 32, TN = BN / WN / 32, TK = BK / 16;
+  static constexpr int KC = BK / 8;                       // A chunks per row
+  static constexpr int NCB = BN / 8;                      // B chunks per row
+  static constexpr int A_DMA = BM * KC / NT;              // copies per thread per stage
+  static constexpr int B_DMA = BK * NCB / NT;
+  static constexpr int D = A_DMA + B_DMA;
+  static constexpr int A_ELEMS = BM * BK, STAGE = BM * BK + BK * BN;
+  static constexpr int LDS_BYTES = S * STAGE * 2;
+  static constexpr int ASH = KC >= 16 ? 0 : (KC == 8 ? 1 : (KC == 4 ? 2 : 3));
+  static constexpr int AMASK = (KC < 16 ? KC : 16) - 1;
+  static constexpr int RP = BN >= 128 ? 1 : 128 / BN;     // B rows per 256 bytes
+  static constexpr int RSH = RP == 1 ? 0 : (RP == 2 ? 1 : 2);
+  static constexpr int RMASK = 4 / RP - 1;
+  static_assert(TM >= 1 && TN >= 1 && TK >= 1, "tile too small for 32x32x16 MFMA");
+  static_assert((BM * KC) % NT == 0 && (BK * NCB) % NT == 0, "tile/thread mismatch");
+  static_assert(WM * WN * 64 == NT, "warps must tile the block");
+  static_assert(S >= 2 && (S - 2) * D <= 63, "vmcnt range");
+  static_assert(NCB >= 4 * (RMASK + 1), "B swizzle needs the row's chunks");
+
+  static EK_INLINE int a_chunk(int row, int kc) { return row * KC + (kc ^ ((row >> ASH) & AMASK)); }
+  static EK_INLINE int b_chunk(int k, int nc) { return k * NCB + (nc ^ (((k >> RSH) & RMASK) << 2)); }
+
+  // Per-thread copy plan, fixed for the whole loop: the global element offset of each chunk
+  // relative to the k origin, or -1 when the chunk's column lies outside the operand.
+  int a_off[A_DMA], b_off[B_DMA], a_kc[A_DMA];
+
+  EK_INLINE void plan(int lda, int ldb, int N, int m0, int n0, int tid) {
+#pragma unroll
+    for (int i = 0; i < A_DMA; ++i) {
+      const int p = i * NT + tid, row = p / KC;
+      const int kc = (p % KC) ^ ((row >> ASH) & AMASK);
+      a_kc[i] = kc * 8;
+      a_off[i] = (m0 + row) * lda + kc * 8;
+    }
+#pragma unroll
+    for (int i = 0; i < B_DMA; ++i) {
+      const int p = i * NT + tid, k = p / NCB;
+      const int nc = (p % NCB) ^ (((k >> RSH) & RMASK) << 2);
+      const int gn = n0 + nc * 8;
+      b_off[i] = (gn + 8 <= N) ? k * ldb + gn : -1;
+    }
+  }
+
+  // Copies the k-th tile (k = first column of A / row of B) into the stage at LDS byte `st`.
+  EK_INLINE void copy(i32x4 ra, i32x4 rb, int ldb, int K, int k, uint32_t st, int wave) {
+#pragma unroll
+    for (int i = 0; i < A_DMA; ++i) {
+      const int off = (k + a_kc[i] + 8 <= K) ? (a_off[i] + k) * 2 : kOOB;
+      dma16(ra, st + (i * NT + wave * 64) * 16, off);
+    }
+#pragma unroll
+    for (int i = 0; i < B_DMA; ++i) {
+      const int off = b_off[i] >= 0 ? (b_off[i] + k * ldb) * 2 : kOOB;
+      dma16(rb, st + A_ELEMS * 2 + (i * NT + wave * 64) * 16, off);
+    }
+  }
+
+  EK_INLINE void compute(float* acc, const uint16_t* st, int lane, int wm, int wn) {
+    typedef short v4s __attribute__((ext_vector_type(4)));
+    const u32x4* sA = reinterpret_cast<const u32x4*>(st);
+    const uint16_t* sB = st + A_ELEMS;
+    const int r32 = lane & 31, h = lane >> 5;
+    const int g = lane >> 4, ti = (lane >> 2) & 3, tq = lane & 3;
+#pragma unroll
+    for (int kk = 0; kk < TK; ++kk) {
+      T a[TM][8], b[TN][8];
+      const int kc = kk * 2 + h;
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm) {
+        const u32x4 v = sA[a_chunk(wm * (BM / WM) + tm * 32 + r32, kc)];
+        __builtin_memcpy(a[tm], &v, 16);
+      }
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+        const int n = wn * (BN / WN) + tn * 32 + 16 * (g & 1) + 4 * tq;
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const int k = kk * 16 + 8 * (g >> 1) + 4 * half + ti;
+          const uint16_t* src = sB + b_chunk(k, n >> 3) * 8 + (n & 7);
+          const v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) v4s*)(src));
+          __builtin_memcpy(&b[tn][4 * half], &v, 8);
+        }
+      }
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) mfma_32x32x16(&acc[(tm * TN + tn) * 16], a[tm], b[tn]);
+    }
+  }
+
+  // Runs the whole k loop: k = lo, lo + BK, ... < hi.
+  EK_INLINE void run(float* acc, const T* A, int lda, const T* B, int ldb, int M, int N, int K,
+                     int m0, int n0, int lo, int hi, char* smem, int tid) {
+    if (hi <= lo) return;
+    const int niter = (hi - lo + BK - 1) / BK;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave % WM, wn = wave / WM;
+    const i32x4 ra = rsrc_words(A, (uint32_t)M * lda * 2);
+    const i32x4 rb = rsrc_words(B, (uint32_t)K * ldb * 2);
+    const uint16_t* s16 = reinterpret_cast<const uint16_t*>(smem);
+    const uint32_t l0 = lds_addr(smem);
+    plan(lda, ldb, N, m0, n0, tid);
+    __syncthreads();  // earlier users of the LDS are done with it
+    // nothing loaded before the loop is outstanding, so the explicit vmcnt below counts
+    // this loop's copies only
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+#pragma unroll
+    for (int s = 0; s < S - 1; ++s) copy(ra, rb, ldb, K, lo + s * BK, l0 + s * STAGE * 2, wave);
+    for (int it = 0; it < niter; ++it) {
+      // this wave's copies of stage `it` have landed (S - 2 younger stages may still fly),
+      // its reads of the previous stage are complete; then everyone's are.
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((S - 2) * D) : "memory");
+      copy(ra, rb, ldb, K, lo + (it + S - 1) * BK, l0 + ((it + S - 1) % S) * STAGE * 2, wave);
+      compute(acc, s16 + (it % S) * STAGE, lane, wm, wn);
+    }
+    // drain the copies issued past the end before anyone reuses the LDS
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   }
 };
 

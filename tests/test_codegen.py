@@ -113,7 +113,8 @@ def test_descriptor_dot_loop_uses_gemm_template():
     f16 = np.zeros(16, np.float16)
     src = codegen_hip.generate(matmul_desc_kernel.ir_for(
         f16, f16, f16, 4096, 4096, 4096, 4096, 4096, 4096, BM=256, BN=256, BK=64)).source
-    assert "ek::Gemm<_Float16, 256, 256, 64, 2, 2, 256, true>" in src
+    # aligned operands within 2 GiB: the LDS-DMA pipeline (64 KB stages, 2 of them)
+    assert "ek::GemmDma<_Float16, 256, 256, 64, 2, 2, 256, 2>" in src
     # K and N not known to be multiples of 8: the template reads the row tails elementwise
     src3 = codegen_hip.generate(matmul_desc_kernel.ir_for(
         f16, f16, f16, 256, 250, 100, 112, 256, 250, BM=128, BN=128, BK=64)).source
@@ -125,15 +126,27 @@ def test_descriptor_dot_loop_uses_gemm_template():
 
 
 def test_lds_bank_model():
+    """The pattern kernels whose SQ_LDS_BANK_CONFLICT counts fixed the model (conflict
+    cycles = passes above one per pass)."""
     from enceladus_amd.compiler import lds
-    # 16-byte accesses to consecutive 16-byte slots: 8 lanes per pass, conflict-free
-    assert lds.pass_cycles([16 * i for i in range(64)], 16) == 8
-    # 8-byte accesses 128 bytes apart: the 16 lanes of a pass share one bank pair
-    assert lds.pass_cycles([128 * i for i in range(64)], 8) == 4 * 16
-    # one dword read by every lane is a broadcast: two 32-lane passes of one cycle
-    assert lds.pass_cycles([0] * 64, 4) == 2
-    # rows of 144 bytes read 8 bytes wide: rows r and r + 8 collide (2-way)
-    assert lds.pass_cycles([144 * (i % 32) + 8 * (i // 32) for i in range(64)], 8) == 8
+    pc = lds.pass_cycles
+    r128 = lambda f: pc([f(l) for l in range(64)], 16)          # noqa: E731
+    w128 = lambda f: pc([f(l) for l in range(64)], 16, True)    # noqa: E731
+    r64 = lambda f: pc([f(l) for l in range(64)], 8)            # noqa: E731
+    assert r128(lambda l: l * 16) == 4 and w128(lambda l: l * 16) == 8
+    assert r128(lambda l: (l >> 1) * 16 + (l & 1) * 128) - 4 == 0
+    assert r128(lambda l: (l % 8) * 16 + (l // 8) * 256) - 4 == 4
+    gemm_a = lambda l: ((l % 32) * 8 + ((l // 32) ^ (((l % 32) >> 1) & 7))) * 16  # noqa: E731
+    assert r128(gemm_a) - 4 == 0 and w128(gemm_a) - 8 == 8
+    fa_old_v = lambda l: (4 * (l % 32)) * 144 + (l // 32) * 16  # noqa: E731
+    assert r128(fa_old_v) - 4 == 12 and w128(fa_old_v) - 8 == 24
+    assert r64(lambda l: l * 8) == 2
+    assert r64(lambda l: (l % 16) * 8 + (l // 16) * 256) - 2 == 2
+    assert r64(lambda l: (l % 32) * 144 + (l // 32) * 8) - 2 == 2
+    assert r128(lambda l: (l % 4) * 16 + (l // 4) * 128) - 4 == 4
+    assert r128(lambda l: (l % 2) * 16 + (l // 2) * 256) - 4 == 28
+    # one dword read by every lane is a broadcast
+    assert pc([0] * 64, 4) == 1
 
 
 @pytest.mark.parametrize("head_dim,block_n", [(128, 64), (64, 64), (128, 32), (64, 128)])
