@@ -1645,16 +1645,26 @@ class Emitter:
     def _frag_read(self, info, lay: LY.Layout, first: str, n: int, dst: str, decl=True):
         """Emits LDS reads of registers [first, first+n) of `lay` from a staged tile."""
         T = info["T"]
+        sm = (f"(reinterpret_cast<const {T}*>({info['smem']}) + (ek_it{info['loop_idx']} % "
+              f"{info['nst']}) * {info['stage_elems']})")
+        if decl:
+            self.emit(f"      {T} {dst}[{n}];")
+        if info.get("dma") and info["mode"] == "trans":
+            # transpose reads: run (first + j) / 4 of the fragment comes from one instruction
+            src = LY.tr16_source(lay)
+            assert src is not None and n % 4 == 0, "fragment layout unfit for transpose reads"
+            r = f"(({first} + j) >> 2)"
+            idx = info["sl"].cexpr(self.coord(src, 0, r), self.coord(src, 1, r))
+            self.emit(f"    #pragma unroll")
+            self.emit(f"    for (int j = 0; j < {n}; j += 4) ek::tr_read4<{T}>(&{dst}[j], "
+                      f"&{sm}[{idx}]);")
+            return
         lay_s = self._stage_view(info, lay)
         d, nb = lay_s.vec_dim_bits()
         V = min(1 << nb, 8, n) if d == info["pos_dim"] else 1
-        sm = (f"(reinterpret_cast<const {T}*>({info['smem']}) + (ek_it{info['loop_idx']} & 1) * "
-              f"{info['stage_elems']})")
         r = f"({first} + j)"
         idx = info["sl"].cexpr(self.coord(lay_s, info["line_dim"], r),
                                self.coord(lay_s, info["pos_dim"], r))
-        if decl:
-            self.emit(f"      {T} {dst}[{n}];")
         self.emit(f"    #pragma unroll")
         self.emit(f"    for (int j = 0; j < {n}; j += {V}) ek::vload<{T}, {V}>(&{dst}[j], "
                   f"&{sm}[{idx}]);")
@@ -1858,11 +1868,133 @@ class Emitter:
         cache[key] = (sl, cyc, LDS.ideal(acc))
         return sl
 
+    def _stage_dma_ok(self, info) -> bool:
+        """Whether a stage can be filled by LDS DMA: buffer-addressable rows of whole 16-byte
+        chunks, a loop-invariant column origin, a chunk count that fills whole wave copies,
+        and (transposed operands) a fragment layout that ds_read_b64_tr_b16 delivers."""
+        if self.opt.get("no_lds_dma"):
+            return False
+        d = self.desc[info["op"].operands[0].id]
+        R, C = info["R"], info["C"]
+        if C % 8 or (R * C // 8) % self.nt or info["kinds"][1] == "iv":
+            return False
+        if not self._stage_buffer_ok(info, d, 8):
+            return False
+        if info["mode"] == "trans":
+            src = LY.tr16_source(info["lay"])
+            if src is None:
+                return False
+            info["tr_src"] = src
+        return True
+
+    def _stage_setup_dma(self, info, idx: int, nst: int):
+        """A stage filled by LDS DMA keeps the tile's memory rows (row-major, 16-byte chunks
+        XOR-swizzled per the bank model); each thread copies `per` chunks per stage. The chunk
+        a lane copies is the one the swizzle puts at its LDS position."""
+        ld = info["op"]
+        d = self.desc[ld.operands[0].id]
+        R, C = info["R"], info["C"]
+        T = ctype(ld.result.type.dtype)
+        info.update({"line_dim": 0, "pos_dim": 1, "W": 8, "dma": True, "nst": nst})
+        nvec = R * C // 8
+        per = nvec // self.nt
+        sl = self._dma_layout(info)
+        name = f"ek_stg{idx}"
+        info.update({"desc": d, "T": T, "sl": sl, "stage_elems": sl.elems, "nvec": nvec,
+                     "per": per, "smem": name})
+        self.extra_smem.append((name, nst * sl.elems * 2))
+        lsh = sl.pitch.bit_length() - 1
+        lensh = C.bit_length() - 1
+        o1 = self._stage_offsets(info, "0")[1]
+        sh1, s0 = d["shape"][1], d["strides"][0]
+        h = (f"((((rw >> {sl.sa}) ^ (rw >> {sl.sb})) & {sl.mask}) << {3 + sl.csh})" if sl.mask
+             else "0")
+        self.emit(f"int ek_dmo{idx}[{per}];")
+        self.emit("#pragma unroll")
+        self.emit(f"for (int i = 0; i < {per}; ++i) {{")
+        self.emit(f"  const int e = (i * {self.nt} + ek_tid) * 8, rw = e >> {lsh};")
+        self.emit(f"  const int vp = (e & {sl.pitch - 1}) ^ {h};")
+        self.emit(f"  const int line = rw * {sl.k} + (vp >> {lensh}), gc = {o1} + (vp & {C - 1});")
+        self.emit(f"  ek_dmo{idx}[i] = (gc >= 0 && gc + 8 <= {sh1}) ? line * {s0} + gc : -1;")
+        self.emit("}")
+        self.emit(f"const uint32_t ek_dml{idx} = ek::lds_addr({name}) + "
+                  f"(uint32_t)__builtin_amdgcn_readfirstlane(ek_warp) * 1024u;")
+
+    def _dma_layout(self, info) -> LDS.StageLayout:
+        """Stage layout for a DMA-filled tile: rows of C elements, chunk swizzle chosen by
+        simulating the dot's fragment reads (16-byte row reads, or transpose reads)."""
+        R, C, lay = info["R"], info["C"], info["lay"]
+        key = ("dma", info["mode"], R, C, self.nt, lay.key())
+        if key in _STAGE_LAYOUTS:
+            return _STAGE_LAYOUTS[key][0]
+        acc = []
+        seen = set()
+        if info["mode"] == "row":
+            d, nb = lay.vec_dim_bits()
+            V = min(1 << nb, 8) if d == 1 else 1
+            for w in range(lay.num_warps):
+                wc = lay.thread_coord(0, w)
+                if wc in seen:
+                    continue
+                seen.add(wc)
+                for j in range(0, lay.nregs, V):
+                    rc = lay.reg_coord(j)
+                    lanes = []
+                    for ln in range(64):
+                        tc = lay.thread_coord(ln, w)
+                        lanes.append((tc[0] | rc[0], tc[1] | rc[1]))
+                    acc.append((2 * V, lanes, False))
+        else:
+            src = info["tr_src"]
+            for w in range(src.num_warps):
+                wc = src.thread_coord(0, w)
+                if wc in seen:
+                    continue
+                seen.add(wc)
+                for j in range(src.nregs):
+                    rc = src.reg_coord(j)
+                    lanes = []
+                    for ln in range(64):
+                        tc = src.thread_coord(ln, w)
+                        lanes.append((tc[0] | rc[0], tc[1] | rc[1]))
+                    acc.append((8, lanes, False))
+        sigma = LDS.identity_sigma(C)
+        best = None
+        for i, c in enumerate(LDS.candidates(R, C, sigma)):
+            if c.pitch != c.rowlen or (R * C) % c.pitch:
+                continue
+            k_ = (LDS.cost(c, acc), c.mask != 0, i)
+            if best is None or k_ < best[0]:
+                best = (k_, c)
+        sl = best[1]
+        _STAGE_LAYOUTS[key] = (sl, best[0][0], LDS.ideal(acc))
+        return sl
+
+    def _stage_dma(self, info, kval: str, stage: str) -> list[str]:
+        """Copies the tile at row origin `kval` (or the loop-invariant one) into stage `stage`.
+        Rows outside [0, shape0) fall past the buffer resource and arrive as zeros."""
+        d = info["desc"]
+        o0, _ = self._stage_offsets(info, kval)
+        idx = info["smem"][len("ek_stg"):]
+        R, per = info["R"], info["per"]
+        base, s0, sh0 = d["base"], d["strides"][0], d["shape"][0]
+        return ["{", f"  const int ek_r0 = {o0};",
+                f"  const ek::i32x4 ek_rs = ek::rsrc_words({base}, (ek_r0 > -{R} && ek_r0 < {sh0})"
+                f" ? (uint32_t){sh0} * (uint32_t){s0} * 2u : 0u);",
+                f"  const int ek_rb = ek_r0 * {s0};",
+                f"  const uint32_t ek_ls = ek_dml{idx} + (uint32_t)({stage}) * "
+                f"{info['stage_elems'] * 2}u;",
+                "  #pragma unroll",
+                f"  for (int i = 0; i < {per}; ++i) ek::dma16(ek_rs, ek_ls + i * {self.nt * 16}, "
+                f"ek_dmo{idx}[i] >= 0 ? (ek_rb + ek_dmo{idx}[i]) * 2 : ek::kOOB);",
+                "}"]
+
     def _stage_setup(self, info, idx: int):
         ld = info["op"]
         d = self.desc[ld.operands[0].id]
         R, C = info["R"], info["C"]
         T = ctype(ld.result.type.dtype)
+        info["nst"] = 2
         if info["mode"] == "row":
             W = 8
             nvec = R * C // 8
@@ -2034,8 +2166,8 @@ class Emitter:
         lay_s = self._stage_view(info, lay)
         d, nb = lay_s.vec_dim_bits()
         V = min(1 << nb, 8) if d == info["pos_dim"] else 1
-        sm = (f"(reinterpret_cast<const {T}*>({info['smem']}) + (ek_it{info['loop_idx']} & 1) * "
-              f"{info['stage_elems']})")
+        sm = (f"(reinterpret_cast<const {T}*>({info['smem']}) + (ek_it{info['loop_idx']} % "
+              f"{info['nst']}) * {info['stage_elems']})")
         idx = info["sl"].cexpr(self.coord(lay_s, info["line_dim"], "r"),
                                self.coord(lay_s, info["pos_dim"], "r"))
         nm = self.fresh("sr")
@@ -2197,7 +2329,30 @@ class Emitter:
         it = ctype(iv.type.dtype)
         ivn = self.fresh("iv")
         stg = self.stage_loops.get(id(op), []) if hasattr(self, "stage_loops") else []
-        if stg:
+        dma = bool(stg) and all(self._stage_dma_ok(info) for info in stg)
+        if dma:
+            li = self.counter
+            self.emit(f"int ek_it{li} = 0;")
+            # stages: 2, or 3 when they fit the LDS share of a workgroup at 8 waves per CU
+            per_stage = sum(info["R"] * info["C"] * 2 for info in stg)
+            share = 163840 // max(1, 8 // (self.nt // 64))
+            nst = int(self.opt.get("stage_count", 0)) or (3 if 3 * per_stage <= share else 2)
+            dcount = sum(info["R"] * info["C"] // 8 // self.nt for info in stg)
+            while nst > 2 and (nst - 2) * dcount > 63:
+                nst -= 1
+            for info in stg:
+                info["loop_idx"] = li
+                self._stage_setup_dma(info, len(self.extra_smem), nst)
+            self.emit("__syncthreads();")
+            # nothing loaded before the loop is outstanding, so the vmcnt at the top of the
+            # body counts this loop's copies only
+            self.emit("__builtin_amdgcn_s_waitcnt(0x0F70);")
+            for s_ in range(nst - 1):
+                for info in stg:
+                    kv = f"({lo} + {s_} * {step})" if s_ else lo
+                    for ln in self._stage_dma(info, kv, str(s_)):
+                        self.emit(ln)
+        elif stg:
             li = self.counter
             self.emit(f"int ek_it{li} = 0;")
             for k, info in enumerate(stg):
@@ -2220,7 +2375,18 @@ class Emitter:
         self.define(iv, ivn)
         for a, nm in zip(carried, names):
             self.define(a, nm)
-        if stg:
+        if dma:
+            self.in_staged_loop = getattr(self, "in_staged_loop", 0) + 1
+            # this wave's copies of the current stage have landed (nst - 2 younger stages may
+            # still fly) and its reads of the previous stage are complete; after the barrier
+            # everyone's are, so the previous stage can be refilled.
+            self.emit(f'asm volatile("s_waitcnt vmcnt({(nst - 2) * dcount}) lgkmcnt(0)\\n\\t'
+                      f's_barrier" ::: "memory");')
+            for info in stg:
+                for ln in self._stage_dma(info, f"({ivn} + {nst - 1} * {step})",
+                                          f"(ek_it{li} + {nst - 1}) % {nst}"):
+                    self.emit(ln)
+        elif stg:
             self.in_staged_loop = getattr(self, "in_staged_loop", 0) + 1
             self.emit(f"const bool ek_more{li} = {ivn} + {step} < {hi};")
             self.emit(f"if (ek_more{li}) {{")
@@ -2229,7 +2395,10 @@ class Emitter:
                     self.emit("  " + ln)
             self.emit("}")
         self.gen_block(body)
-        if stg:
+        if dma:
+            self.emit(f"++ek_it{li};")
+            self.in_staged_loop -= 1
+        elif stg:
             self.emit(f"if (ek_more{li}) {{")
             for info in stg:
                 for ln in self._stage_store(info, f"(ek_it{li} + 1) & 1"):
@@ -2241,6 +2410,9 @@ class Emitter:
         y = body.ops[-1]
         self._assign_yield(y.operands, carried, names)
         self.pop_scope()
+        if dma:
+            # copies issued past the last iteration land before anyone reuses the LDS
+            self.emit('asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\\n\\ts_barrier" ::: "memory");')
         for r, nm in zip(op.results, names):
             self.define(r, nm)
 

@@ -429,3 +429,47 @@ def mfma_operand(plan: DotPlan, which: str) -> Layout:
     lay = Layout(shape, tuple(reg), tuple(lane), tuple(wbits), f"mfma_{which}")
     lay.check()
     return lay
+
+
+def tr16_source(lay: Layout):
+    """The address layout for reading the 16-bit fragment `lay` of a row-major [rows, cols]
+    LDS tile with ds_read_b64_tr_b16, or None when `lay` does not fit that instruction.
+
+    In each group of 16 lanes, ds_read_b64_tr_b16 gives output lane L, value t, element L % 4
+    of the 8-byte read made by lane 4t + L // 4. So a register run of 4 (values t = 0..3)
+    must hold 4 rows, and output lanes 0..3 must hold 4 consecutive columns: the lane that
+    reads for (t, L // 4) supplies row k(t) and the first of the 4 columns of lanes
+    4 (L // 4) + 0..3. The returned layout maps those address lanes (bits 0,1 <- output lane
+    bits 2,3; bits 2,3 <- value t; bits 4,5 <- output lane bits 4,5) and the run index
+    (register bits) to (row, column) coordinates."""
+    if len(lay.shape) != 2 or len(lay.reg) < 2:
+        return None
+    if lay.reg[0][0] != 0 or lay.reg[1][0] != 0:
+        return None
+    if lay.lane[0] != (1, 0) or lay.lane[1] != (1, 1):
+        return None
+    if any(b is None or b[0] != 1 for b in lay.lane[2:4]):
+        return None
+    lane = (lay.lane[2], lay.lane[3], lay.reg[0], lay.reg[1], lay.lane[4], lay.lane[5])
+    src = Layout(lay.shape, tuple(lay.reg[2:]), lane, lay.warp, "tr16")
+    if not tr16_check(lay, src):
+        return None
+    return src
+
+
+def tr16_check(lay: Layout, src: Layout) -> bool:
+    """Every output lane/value of the transpose read at `src` addresses equals `lay`."""
+    for w in range(lay.num_warps):
+        for run in range(lay.nregs // 4):
+            for ln in range(64):
+                for t in range(4):
+                    tc = lay.thread_coord(ln, w)
+                    rc = lay.reg_coord(run * 4 + t)
+                    want = (tc[0] | rc[0], tc[1] | rc[1])
+                    prov = 16 * (ln // 16) + 4 * t + (ln % 16) // 4
+                    ptc = src.thread_coord(prov, w)
+                    prc = src.reg_coord(run)
+                    got = (ptc[0] | prc[0], (ptc[1] | prc[1]) + ln % 4)
+                    if got != want:
+                        return False
+    return True

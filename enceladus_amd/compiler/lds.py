@@ -8,8 +8,10 @@ packed `k = 64 / length` to a row, so that every row spans all 32 banks; the 16-
 index inside a row is then XOR-swizzled by a function of the row:
 
     row = line // k,  vp = (line % k) * length + sp
-    offset(line, sp) = row * pitch + (vp ^ (h(row) << 3)),
+    offset(line, sp) = row * pitch + (vp ^ (h(row) << (3 + csh))),
     h(row) = ((row >> sa) ^ (row >> sb)) & mask
+
+(`csh` > 0 moves whole groups of 2^csh chunks, which transpose reads of 4 rows need.)
 
 Bank model (gfx950 LDS, measured with SQ_LDS_BANK_CONFLICT on access-pattern kernels): a
 read is served 256 bytes per cycle (64 banks of 4 bytes): 16 lanes per pass for 16-byte
@@ -40,6 +42,7 @@ class StageLayout:
     sb: int = NO_SHIFT
     sigma: tuple = ()    # sigma[i] = storage bit of logical position bit i
     rowlen: int = 64     # lines shorter than this are packed to rows of `rowlen` elements
+    csh: int = 0         # the swizzle XORs chunk groups of 2^csh chunks
 
     @property
     def k(self) -> int:
@@ -75,14 +78,14 @@ class StageLayout:
 
     def offset(self, line: int, sp: int) -> int:
         row, vp = line // self.k, (line % self.k) * self.length + sp
-        return row * self.pitch + (vp ^ (self.h(row) << 3))
+        return row * self.pitch + (vp ^ (self.h(row) << (3 + self.csh)))
 
     def cexpr(self, line: str, sp: str) -> str:
         """C++ element offset for the line and storage-position expressions."""
         lsh = self.k.bit_length() - 1  # lines per row = 2^lsh
         lensh = self.length.bit_length() - 1
-        return (f"ek::swz<{self.pitch}, {self.mask}, {self.sa}, {self.sb}, {lsh}, {lensh}>"
-                f"({line}, {sp})")
+        return (f"ek::swz<{self.pitch}, {self.mask}, {self.sa}, {self.sb}, {lsh}, {lensh}, "
+                f"{self.csh}>({line}, {sp})")
 
 
 def identity_sigma(length: int) -> tuple:
@@ -147,12 +150,15 @@ def candidates(lines: int, length: int, sigma: tuple) -> list[StageLayout]:
             continue
         out += [StageLayout(lines, length, rowlen + 8, sigma=sigma, rowlen=rowlen),
                 StageLayout(lines, length, rowlen, sigma=sigma, rowlen=rowlen)]
-        m = min(rowlen // 8, 16) - 1
-        for a in range(5):
-            out.append(StageLayout(lines, length, rowlen, m, a, NO_SHIFT, sigma, rowlen))
-        for a in range(4):
-            for b in range(a + 1, 7):
-                out.append(StageLayout(lines, length, rowlen, m, a, b, sigma, rowlen))
+        for csh in (0, 1, 2):
+            m = (min(rowlen // 8, 16) >> csh) - 1
+            if m <= 0:
+                continue
+            for a in range(5):
+                out.append(StageLayout(lines, length, rowlen, m, a, NO_SHIFT, sigma, rowlen, csh))
+            for a in range(4):
+                for b in range(a + 1, 7):
+                    out.append(StageLayout(lines, length, rowlen, m, a, b, sigma, rowlen, csh))
     return out
 
 

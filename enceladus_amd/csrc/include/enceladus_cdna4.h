@@ -399,16 +399,16 @@ EK_INLINE void transpose8x4(const u32x2* r, u32x4* o) {
 }
 
 // Element offset in a staged LDS tile. Lines of 2^LENSH elements are packed 2^LSH to a row of
-// PITCH elements; the 8-element chunk of a position inside its row is XOR-swizzled by
-// ((row >> SA) ^ (row >> SB)) & MASK.
-template <int PITCH, int MASK, int SA, int SB, int LSH, int LENSH>
+// PITCH elements; inside its row, a position's group of 2^CSH 8-element chunks is XOR-swizzled
+// by ((row >> SA) ^ (row >> SB)) & MASK.
+template <int PITCH, int MASK, int SA, int SB, int LSH, int LENSH, int CSH = 0>
 EK_INLINE int swz(int line, int sp) {
   const int row = line >> LSH;
   const int vp = ((line & ((1 << LSH) - 1)) << LENSH) | sp;
   if constexpr (MASK == 0) {
     return row * PITCH + vp;
   } else {
-    return row * PITCH + (vp ^ ((((row >> SA) ^ (row >> SB)) & MASK) << 3));
+    return row * PITCH + (vp ^ ((((row >> SA) ^ (row >> SB)) & MASK) << (3 + CSH)));
   }
 }
 
@@ -426,6 +426,16 @@ EK_INLINE u32x2 buffer_load8(__amdgpu_buffer_rsrc_t r, int byte_off) {
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, 0));
 }
 constexpr int kOOB = 0x7ffffff0;  // an offset past any resource: loads read zeros
+
+// ds_read_b64_tr_b16: in each group of 16 lanes, output lane L receives element L % 4 of the
+// 8-byte LDS reads made by lanes 4t + L / 4, t = 0..3 (a 4x4 transpose of 16-bit elements).
+template <typename T>
+EK_INLINE void tr_read4(T* dst, const T* src) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  const v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4s*)(src));
+  __builtin_memcpy(dst, &v, 8);
+}
 
 // Buffer resource as four SGPR words, for the inline-asm copy below.
 typedef int i32x4 __attribute__((ext_vector_type(4)));

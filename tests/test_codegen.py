@@ -170,3 +170,18 @@ def test_attention_stage_layouts_are_bijective_and_conflict_free(head_dim, block
         # a 16-byte chunk stays contiguous under the swizzle
         assert all(sl.offset(ln, 8 * c + e) == sl.offset(ln, 8 * c) + e
                    for ln in range(sl.lines) for c in range(sl.length // 8) for e in range(8))
+
+
+def test_transpose_read_source_layouts():
+    """ds_read_b64_tr_b16 (measured on gfx950: in each 16-lane group, output lane L, value t
+    is element L % 4 of the read by lane 4t + L // 4) delivers the MFMA B fragments of a
+    row-major LDS tile, including the attention PV operand's permuted k order; A fragments
+    (k along registers, rows along lanes) do not fit it."""
+    for bm, bn, bk, nw, dw, tr, ko in [(128, 128, 64, 4, (4, 1), True, (0, 1, 3, 2, 4, 5)),
+                                       (256, 256, 64, 8, (4, 2), False, ()),
+                                       (128, 64, 128, 4, (4, 1), True, ())]:
+        plan = L.plan_dot(bm, bn, bk, nw, "bfloat16", dot_warps=dw, trans=tr, korder=ko)
+        lb = L.mfma_operand(plan, "b")
+        src = L.tr16_source(lb)
+        assert src is not None and L.tr16_check(lb, src)
+        assert L.tr16_source(L.mfma_operand(plan, "a")) is None
