@@ -126,7 +126,7 @@ def w_softmax(torch, timer, steps, warmup):
         make_launch(softmax_kernel, (M,), (o, x, N, N, N), BLOCK=8192, num_warps=nw)
         for x, o in zip(xs, outs)])
     return {"name": "softmax", "config": f"fp32 [4096, 8192] num_warps={nw}", "ms": ms,
-            "bytes": nbytes, "gbps": nbytes / ms / 1e6, "bound": "hbm",
+            "bytes": nbytes, "gbps": nbytes / ms / 1e6, "dtype": "fp32", "bound": "hbm",
             "kernel": launches[0].ck.name}
 
 
@@ -143,7 +143,7 @@ def w_rmsnorm(torch, timer, steps, warmup):
         make_launch(rmsnorm_kernel, (M,), (x, w, o, N, N, N, 1e-6), BLOCK=8192, num_warps=nw)
         for x, o in zip(xs, outs)])
     return {"name": "rmsnorm", "config": f"fp32 [4096, 8192] eps 1e-6 num_warps={nw}", "ms": ms,
-            "bytes": nbytes, "gbps": nbytes / ms / 1e6, "bound": "hbm",
+            "bytes": nbytes, "gbps": nbytes / ms / 1e6, "dtype": "fp32", "bound": "hbm",
             "kernel": launches[0].ck.name}
 
 
@@ -157,7 +157,7 @@ def w_vector_add(torch, timer, steps, warmup):
     launches = [make_launch(add_kernel, (n // 1024,), (x, y, out, n), BLOCK=1024) for x in xs]
     ms = timer.run(launches, max(4, steps // 4), max(2, warmup // 4))
     return {"name": "vector_add", "config": "fp32 n=2^28 BLOCK 1024", "ms": ms,
-            "bytes": nbytes, "gbps": nbytes / ms / 1e6, "bound": "hbm",
+            "bytes": nbytes, "gbps": nbytes / ms / 1e6, "dtype": "fp32", "bound": "hbm",
             "kernel": launches[0].ck.name}
 
 
@@ -186,7 +186,7 @@ def w_matmul(torch, timer, steps, warmup, fused=False):
     flop = 2 * M * N * K
     return {"name": "matmul_gelu" if fused else "matmul", "config": "fp16 4096^3 fp32 acc"
             + (" + bias + GELU" if fused else "") + f" {cfg}", "ms": ms, "flop": flop,
-            "tflops": flop / ms / 1e9, "bound": "mfma", "kernel": l.ck.name}
+            "tflops": flop / ms / 1e9, "dtype": "fp16", "bound": "mfma", "kernel": l.ck.name}
 
 
 def w_attention(torch, timer, steps, warmup, causal=True, n=4096):
@@ -209,7 +209,7 @@ def w_attention(torch, timer, steps, warmup, causal=True, n=4096):
     return {"name": f"attention_{'causal' if causal else 'noncausal'}_{n}",
             "config": f"bf16 [4,32,{n},128] {'causal' if causal else 'non-causal'} "
                       f"BLOCK_M/N/warps={cfg}", "ms": ms,
-            "flop": flop, "tflops": flop / ms / 1e9, "bound": "mfma", "kernel": l.ck.name}
+            "flop": flop, "tflops": flop / ms / 1e9, "dtype": "bf16", "bound": "mfma", "kernel": l.ck.name}
 
 
 def w_histogram(torch, timer, steps, warmup):
@@ -224,7 +224,7 @@ def w_histogram(torch, timer, steps, warmup):
     nbytes = 4 * n
     return {"name": "histogram", "config": f"int32 2^26 -> 1024 bins num_warps={nw}", "ms": ms,
             "bytes": nbytes,
-            "gbps": nbytes / ms / 1e6, "bound": "hbm", "kernel": launches[0].ck.name}
+            "gbps": nbytes / ms / 1e6, "dtype": "int32", "bound": "hbm", "kernel": launches[0].ck.name}
 
 
 def w_cumsum(torch, timer, steps, warmup):
@@ -240,7 +240,7 @@ def w_cumsum(torch, timer, steps, warmup):
                     BLOCK_N=4096, num_warps=nw) for x, o in zip(xs, outs)])
     return {"name": "cumsum", "config": f"int32 [8192, 4096] rows num_warps={nw}", "ms": ms,
             "bytes": nbytes,
-            "gbps": nbytes / ms / 1e6, "bound": "hbm", "kernel": launches[0].ck.name}
+            "gbps": nbytes / ms / 1e6, "dtype": "int32", "bound": "hbm", "kernel": launches[0].ck.name}
 
 
 def w_torch_matmul(torch, timer, steps, warmup):
@@ -252,8 +252,23 @@ def w_torch_matmul(torch, timer, steps, warmup):
     ms = timer.run([lambda: torch.matmul(a, b, out=c)], max(5, steps // 2), 3)
     flop = 2 * M * N * K
     return {"name": "torch_matmul", "config": "hipBLASLt fp16 4096^3 (calibration, not ours)",
-            "ms": ms, "flop": flop, "tflops": flop / ms / 1e9, "bound": "mfma",
+            "ms": ms, "flop": flop, "tflops": flop / ms / 1e9, "dtype": "fp16", "bound": "mfma",
             "kernel": "torch.matmul"}
+
+
+def w_torch_attention(torch, timer, steps, warmup, causal=True, n=4096):
+    """Calibration only: torch's scaled_dot_product_attention (its ROCm flash kernel) on
+    the same bf16 [4, 32, n, 128] problem."""
+    import torch.nn.functional as F
+    B, H, D = 4, 32, 128
+    q, k, v = (torch.randn(B, H, n, D, device="cuda").bfloat16() for _ in range(3))
+    ms = timer.run([lambda: F.scaled_dot_product_attention(q, k, v, is_causal=causal)],
+                   max(3, steps // 4), 2)
+    flop = 4 * B * H * n * n * D // (2 if causal else 1)
+    return {"name": "torch_attention", "config": f"torch SDPA bf16 [4,32,{n},128] "
+            f"{'causal' if causal else 'non-causal'} (calibration, not ours)", "ms": ms,
+            "flop": flop, "tflops": flop / ms / 1e9, "dtype": "bf16", "bound": "mfma",
+            "kernel": "torch.sdpa"}
 
 
 def w_copy_calib(torch, timer, steps, warmup):
@@ -264,7 +279,7 @@ def w_copy_calib(torch, timer, steps, warmup):
     ms = timer.run([lambda: y.copy_(x)], max(4, steps // 4), 2)
     nbytes = 8 * n
     return {"name": "copy_calib", "config": "torch copy 256 MiB -> 256 MiB", "ms": ms,
-            "bytes": nbytes, "gbps": nbytes / ms / 1e6, "bound": "hbm", "kernel": "copy"}
+            "bytes": nbytes, "gbps": nbytes / ms / 1e6, "dtype": "fp32", "bound": "hbm", "kernel": "copy"}
 
 
 WORKLOADS = {
@@ -275,9 +290,10 @@ WORKLOADS = {
     "attention_noncausal": lambda t, tm, s, w: w_attention(t, tm, s, w, False, 1024),
     "histogram": w_histogram, "cumsum": w_cumsum,
     "torch_matmul": w_torch_matmul,
+    "torch_attention": w_torch_attention,
     "copy_calib": w_copy_calib,
 }
-DEFAULT = [k for k in WORKLOADS if k not in ("torch_matmul", "copy_calib")]
+DEFAULT = [k for k in WORKLOADS if k not in ("torch_matmul", "torch_attention", "copy_calib")]
 
 
 def measured_traffic(kernel: str):
@@ -359,12 +375,14 @@ def main():
         "unit": "GB/s" if "gbps" in head else "TFLOP/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(head["ms"], 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+        "vs_baseline": None, "dtype": head.get("dtype", "fp32"), "data": "synthetic",
         "config": {"workload": f"{head['name']} {head['config']}",
                    "device": info.name.decode(), "arch": info.arch.decode(),
                    "cus": info.compute_units},
-        "roofline": {"bound": head["bound"], "achieved": round(head.get("gbps", 0.0), 1),
-                     "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+        "roofline": ({"bound": "hbm", "achieved": round(head["gbps"], 1),
+                      "peak": HBM_PEAK / 1e9, "unit": "GB/s"} if head["bound"] == "hbm" else
+                     {"bound": "mfma", "achieved": round(head["tflops"], 1),
+                      "peak": MFMA_PEAK_F16 / 1e12, "unit": "TFLOP/s"}) | {
                      "frac": round(head["roofline_frac"], 4),
                      "traffic": measured_traffic(head["kernel"])},
         "workloads": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
