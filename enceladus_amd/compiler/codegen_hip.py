@@ -138,7 +138,7 @@ class GeneratedKernel:
     num_warps: int
     lds_bytes: int
     block: int
-    coarsen: int = 1
+    coarsen: int = 0       # workgroups per CU of a coarsened launch (0: one per program)
 
 
 class Emitter:
@@ -958,27 +958,43 @@ class Emitter:
         self.prime(*[(o, lay) for o in op.operands])
         nm = self.fresh("ld")
         self.emit(f"{t} {nm}[{lay.nregs}];")
-        self.emit("#pragma unroll")
         hdr = f"for (int rv = 0; rv < {lay.nregs}; rv += {V}) {{"
-        self.emit(hdr)
         pe = lambda i: self.elem(ptr, lay, f"rv + {i}" if i else "rv")  # noqa: E731
         ld = "vload_nt" if self._streaming_load(op) else "vload"
-        if len(op.operands) == 1:
+
+        def plain():
+            self.emit("#pragma unroll")
+            self.emit(hdr)
             self.emit(f"  ek::{ld}<{t}, {V}>(&{nm}[rv], {pe(0)});")
+            self.emit("}")
+        if len(op.operands) == 1:
+            plain()
+            self.define(res, nm)
+            return
+        mask, other = op.operands[1], op.operands[2]
+        # Edge versioning: a mask that is provably all-true over a uniform runtime interval
+        # (e.g. offs < n away from the last program) gets a branch-free unmasked path.
+        cond = None if self.opt.get("no_edge_versioning") else self.all_true(mask)
+        if cond:
+            self.emit(f"if ({cond}) {{")
+            plain()
+            self.emit("} else {")
+        me = lambda i: self.elem(mask, lay, f"rv + {i}" if i else "rv")  # noqa: E731
+        oe = lambda i: self.elem(other, lay, f"rv + {i}" if i else "rv")  # noqa: E731
+        self.emit("#pragma unroll")
+        self.emit(hdr)
+        if V > 1:
+            allm = " && ".join(f"({me(i)})" for i in range(V))
+            self.emit(f"  if ({allm}) {{ ek::{ld}<{t}, {V}>(&{nm}[rv], {pe(0)}); }}")
+            self.emit("  else {")
+            for i in range(V):
+                self.emit(f"    {nm}[rv + {i}] = ({me(i)}) ? *({pe(i)}) : {oe(i)};")
+            self.emit("  }")
         else:
-            mask, other = op.operands[1], op.operands[2]
-            me = lambda i: self.elem(mask, lay, f"rv + {i}" if i else "rv")  # noqa: E731
-            oe = lambda i: self.elem(other, lay, f"rv + {i}" if i else "rv")  # noqa: E731
-            if V > 1:
-                allm = " && ".join(f"({me(i)})" for i in range(V))
-                self.emit(f"  if ({allm}) {{ ek::{ld}<{t}, {V}>(&{nm}[rv], {pe(0)}); }}")
-                self.emit("  else {")
-                for i in range(V):
-                    self.emit(f"    {nm}[rv + {i}] = ({me(i)}) ? *({pe(i)}) : {oe(i)};")
-                self.emit("  }")
-            else:
-                self.emit(f"  {nm}[rv] = ({me(0)}) ? *({pe(0)}) : {oe(0)};")
+            self.emit(f"  {nm}[rv] = ({me(0)}) ? *({pe(0)}) : {oe(0)};")
         self.emit("}")
+        if cond:
+            self.emit("}")
         self.define(res, nm)
 
     def _depends_on_pid(self, v: ir.Value, depth=0) -> bool:
@@ -1019,9 +1035,19 @@ class Emitter:
         vals = self.array(val, lay)
         if own:
             self.emit(f"if ({own}) {{")
+        st = "vstore" if self.opt.get("no_nt_stores") else "vstore_nt"
+        cond = None
+        if mask is not None and not self.opt.get("no_edge_versioning"):
+            cond = self.all_true(mask)
+        if cond:
+            # edge versioning, as for loads
+            self.emit(f"if ({cond}) {{")
+            self.emit("#pragma unroll")
+            self.emit(f"for (int rv = 0; rv < {lay.nregs}; rv += {V}) "
+                      f"ek::{st}<{t}, {V}>({pe(0)}, &{vals}[rv]);")
+            self.emit("} else {")
         self.emit("#pragma unroll")
         self.emit(f"for (int rv = 0; rv < {lay.nregs}; rv += {V}) {{")
-        st = "vstore" if self.opt.get("no_nt_stores") else "vstore_nt"
         if mask is None:
             self.emit(f"  ek::{st}<{t}, {V}>({pe(0)}, &{vals}[rv]);")
         else:
@@ -1036,6 +1062,8 @@ class Emitter:
             else:
                 self.emit(f"  if ({me(0)}) *({pe(0)}) = {vals}[rv];")
         self.emit("}")
+        if cond:
+            self.emit("}")
         if own:
             self.emit("}")
 
@@ -1266,10 +1294,18 @@ class Emitter:
                 elif k == "gt" and same(b) and isinstance(self._const_of(a), int):
                     hi = self._const_of(a)
             if lo_ok and hi is not None and 0 < hi <= 16384:
-                self.priv[op.result.id] = {"base": base, "bins": hi, "dt": dt}
+                self.priv[op.result.id] = {"base": base, "bins": hi, "dt": dt,
+                                           "name": f"ek_bins{len(self.priv)}"}
         if self.priv:
-            self.n_bins = max(i["bins"] for i in self.priv.values())
-            self.coarsen = not self.opt.get("no_coarsen")
+            # Copies (option `priv_copies`): bin b's copy c sits at word b * C + c and lane
+            # l adds into copy l % C. Measured on the 1024-bin histogram, one copy and 8
+            # workgroups per CU is fastest: the loop is bound by loads in flight, and extra
+            # copies cost occupancy and flush work.
+            words = sum(i["bins"] for i in self.priv.values())
+            wgs = int(self.opt.get("priv_wgs", 8))
+            cop = int(self.opt.get("priv_copies", 1))
+            self.priv_copies = cop
+            self.coarsen = 0 if self.opt.get("no_coarsen") else wgs
 
     # -- atomics --------------------------------------------------------------------
     def _atomic_call(self, kind: str, t: str, dt: core.dtype, p: str, v: str, cmp=None) -> str:
@@ -1340,9 +1376,15 @@ class Emitter:
             conds.append(f"({self.elem(mask, lay, 'r')})")
             ie = self.elem(idx, lay, "r")
             ve = self.elem(val_v, lay, "r")
+            cop = self.priv_copies
+            # Branch-free: a masked-off lane adds 0 to bin 0 (the mask bounds the index, so
+            # an unmasked index is always a valid bin), which keeps the loop one basic block.
+            ie = f"(({' && '.join(conds)}) ? ({ie}) : 0)"
+            ve = f"(({' && '.join(conds)}) ? ({ve}) : 0)"
+            slot = f"{ie} * {cop} + (ek_lane & {cop - 1})" if cop > 1 else ie
             self.emit("#pragma unroll")
-            self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) if ({' && '.join(conds)}) "
-                      f"__hip_atomic_fetch_add(&ek_bins{pv['dt'].name}[{ie}], {ve}, "
+            self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) "
+                      f"__hip_atomic_fetch_add(&{pv['name']}[{slot}], {ve}, "
                       f"__ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);")
             self.define(res, "ek_unused")
             return
@@ -2512,7 +2554,8 @@ class Emitter:
             self.def_level[a.id] = 0
         self.plan_dots(fn)
         self.plan_staging(fn.body)
-        self.coarsen = bool(self.opt.get("coarsen"))
+        # workgroups per CU for a coarsened grid (0: one workgroup per program)
+        self.coarsen = 4 if self.opt.get("coarsen") else 0
         self.plan_privatization(fn)
         self.assign_block(fn.body)
         self.remap_pids = bool(self.dot_plans) and not self.opt.get("no_pid_remap") and \
@@ -2562,40 +2605,62 @@ class Emitter:
                     yield it
         body = list(flat(self.scopes[0].items))
         if self.priv:
-            dts = sorted({i["dt"].name for i in self.priv.values()})
-            for dn in dts:
-                out.append(f"  __shared__ {'int32_t' if dn == 'i32' else 'uint32_t'} "
-                           f"ek_bins{dn}[{self.n_bins}];")
-                out.append(f"  for (int i = ek_tid; i < {self.n_bins}; i += {self.nt}) "
-                           f"ek_bins{dn}[i] = 0;")
+            cop = self.priv_copies
+            for info in self.priv.values():
+                t = "int32_t" if info["dt"].name == "i32" else "uint32_t"
+                n = info["bins"] * cop
+                out.append(f"  __shared__ __attribute__((aligned(16))) {t} {info['name']}[{n}];")
+                out.append(f"  for (int i = ek_tid; i < {n}; i += {self.nt}) {info['name']}[i] = 0;")
             out.append("  __syncthreads();")
         if self.coarsen:
             # Program coarsening: a capped grid of workgroups walks the logical program ids
-            # (programs are independent; privatised atomics commute).
+            # (programs are independent; privatised atomics commute). The walk is unrolled
+            # by U programs, each in its own scope, so the compiler can issue the U
+            # programs' global loads before the first program's LDS atomics: a workgroup
+            # keeps U loads in flight instead of one.
+            u_ = max(1, int(self.opt.get("coarsen_unroll", 4)))
+            pids = ["  const int ek_pid_x = ek_p % ek_np_x;",
+                    "  const int ek_pid_y = (ek_p / ek_np_x) % ek_np_y;",
+                    "  const int ek_pid_z = ek_p / (ek_np_x * ek_np_y);",
+                    "  (void)ek_pid_x; (void)ek_pid_y; (void)ek_pid_z;"]
             out.append("  const int ek_nprog = ek_np_x * ek_np_y * ek_np_z;")
-            out.append("  for (int ek_p = blockIdx.x; ek_p < ek_nprog; ek_p += gridDim.x) {")
-            out.append("  const int ek_pid_x = ek_p % ek_np_x;")
-            out.append("  const int ek_pid_y = (ek_p / ek_np_x) % ek_np_y;")
-            out.append("  const int ek_pid_z = ek_p / (ek_np_x * ek_np_y);")
-            out.append("  (void)ek_pid_x; (void)ek_pid_y; (void)ek_pid_z;")
+            out.append("  const int ek_g = (int)gridDim.x;")
+            out.append("  int ek_p0 = blockIdx.x;")
+            if u_ > 1:
+                out.append(f"  for (; ek_p0 + {u_ - 1} * ek_g < ek_nprog; ek_p0 += {u_} * ek_g) {{")
+                for k_ in range(u_):
+                    out.append(f"  {{ const int ek_p = ek_p0 + {k_} * ek_g;")
+                    out.extend(pids)
+                    out.extend(body)
+                    out.append("  }")
+                out.append("  }")
+            out.append("  for (int ek_p = ek_p0; ek_p < ek_nprog; ek_p += ek_g) {")
+            out.extend(pids)
             out.extend(body)
             out.append("  }")
         else:
             out.extend(body)
         if self.priv:
+            # Flush: a wave reads consecutive words (whole groups of C copies), sums each group
+            # with butterfly shuffles and one lane adds the bin's total to global memory.
             out.append("  __syncthreads();")
+            cop = self.priv_copies
             for rid, info in self.priv.items():
-                dn = info["dt"].name
                 base = self.name[info["base"].id]
-                out.append(f"  for (int i = ek_tid; i < {info['bins']}; i += {self.nt}) {{")
-                out.append(f"    const auto v = ek_bins{dn}[i];")
-                out.append(f"    if (v) __hip_atomic_fetch_add({base} + i, v, __ATOMIC_RELAXED, "
+                n = info["bins"] * cop
+                out.append(f"  for (int i = ek_tid; i < {(n + 63) // 64 * 64}; i += {self.nt}) {{")
+                out.append(f"    auto v = i < {n} ? {info['name']}[i] : 0;")
+                o = 1
+                while o < cop:
+                    out.append(f"    v += ek::shfl(v, ek_lane ^ {o});")
+                    o *= 2
+                out.append(f"    if (i < {n} && (i & {cop - 1}) == 0 && v) "
+                           f"__hip_atomic_fetch_add({base} + i / {cop}, v, __ATOMIC_RELAXED, "
                            "__HIP_MEMORY_SCOPE_AGENT);")
                 out.append("  }")
-                break
         out.append("}")
         gk = GeneratedKernel(kname, "\n".join(out) + "\n", args, self.nw, self.lds, self.nt)
-        gk.coarsen = 1 if self.coarsen else 0
+        gk.coarsen = int(self.coarsen)
         return gk
 
 

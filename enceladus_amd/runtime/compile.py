@@ -139,7 +139,7 @@ class CompiledKernel:
         if not self.gen.coarsen:
             return (gx, gy, gz), b""
         total = gx * gy * gz
-        cap = max(1, coarsen_cap())
+        cap = max(1, coarsen_cap() * self.gen.coarsen)
         import struct
         return (min(total, cap), 1, 1), struct.pack("<iii", gx, gy, gz)
 
@@ -160,13 +160,13 @@ _CAP = None
 
 
 def coarsen_cap() -> int:
-    """Workgroups for coarsened kernels: 4 per compute unit of GPU 0."""
+    """Compute units of GPU 0: a coarsened kernel launches `gen.coarsen` workgroups per CU."""
     global _CAP
     if _CAP is None:
         try:
-            _CAP = 4 * hip.device_info(0).compute_units
+            _CAP = hip.device_info(0).compute_units
         except Exception:  # noqa: BLE001
-            _CAP = 1024
+            _CAP = 256
     return _CAP
 
 
