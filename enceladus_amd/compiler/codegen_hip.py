@@ -1959,6 +1959,11 @@ class Emitter:
         self.emit(f"  const int line = rw * {sl.k} + (vp >> {lensh}), gc = {o1} + (vp & {C - 1});")
         self.emit(f"  ek_dmo{idx}[i] = (gc >= 0 && gc + 8 <= {sh1}) ? line * {s0} + gc : -1;")
         self.emit("}")
+        # byte offsets relative to the tile's first row, for the resource that starts there
+        self.emit(f"int ek_dmb{idx}[{per}];")
+        self.emit("#pragma unroll")
+        self.emit(f"for (int i = 0; i < {per}; ++i) "
+                  f"ek_dmb{idx}[i] = ek_dmo{idx}[i] >= 0 ? ek_dmo{idx}[i] * 2 : ek::kOOB;")
         self.emit(f"const uint32_t ek_dml{idx} = ek::lds_addr({name}) + "
                   f"(uint32_t)__builtin_amdgcn_readfirstlane(ek_warp) * 1024u;")
 
@@ -2020,15 +2025,26 @@ class Emitter:
         idx = info["smem"][len("ek_stg"):]
         R, per = info["R"], info["per"]
         base, s0, sh0 = d["base"], d["strides"][0], d["shape"][0]
+        # A tile starting at row >= 0 (the usual case) copies through a resource based at its
+        # first row, so the per-chunk offsets are loop-invariant; otherwise rows before 0
+        # need the general form with the row offset in each lane's address.
         return ["{", f"  const int ek_r0 = {o0};",
-                f"  const ek::i32x4 ek_rs = ek::rsrc_words({base}, (ek_r0 > -{R} && ek_r0 < {sh0})"
-                f" ? (uint32_t){sh0} * (uint32_t){s0} * 2u : 0u);",
-                f"  const int ek_rb = ek_r0 * {s0};",
                 f"  const uint32_t ek_ls = ek_dml{idx} + (uint32_t)({stage}) * "
                 f"{info['stage_elems'] * 2}u;",
-                "  #pragma unroll",
-                f"  for (int i = 0; i < {per}; ++i) ek::dma16(ek_rs, ek_ls + i * {self.nt * 16}, "
+                "  if (ek_r0 >= 0) {",
+                f"    const ek::i32x4 ek_rs = ek::rsrc_words({base} + (int64_t)ek_r0 * {s0}, "
+                f"ek_r0 < {sh0} ? (uint32_t)({sh0} - ek_r0) * (uint32_t){s0} * 2u : 0u);",
+                "    #pragma unroll",
+                f"    for (int i = 0; i < {per}; ++i) ek::dma16(ek_rs, ek_ls + i * {self.nt * 16}, "
+                f"ek_dmb{idx}[i]);",
+                "  } else {",
+                f"    const ek::i32x4 ek_rs = ek::rsrc_words({base}, ek_r0 > -{R} ? "
+                f"(uint32_t){sh0} * (uint32_t){s0} * 2u : 0u);",
+                f"    const int ek_rb = ek_r0 * {s0};",
+                "    #pragma unroll",
+                f"    for (int i = 0; i < {per}; ++i) ek::dma16(ek_rs, ek_ls + i * {self.nt * 16}, "
                 f"ek_dmo{idx}[i] >= 0 ? (ek_rb + ek_dmo{idx}[i]) * 2 : ek::kOOB);",
+                "  }",
                 "}"]
 
     def _stage_setup(self, info, idx: int):

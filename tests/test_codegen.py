@@ -185,3 +185,12 @@ def test_transpose_read_source_layouts():
         src = L.tr16_source(lb)
         assert src is not None and L.tr16_check(lb, src)
         assert L.tr16_source(L.mfma_operand(plan, "a")) is None
+
+
+def test_two_privatised_histograms_get_their_own_bins():
+    from tests.test_gpu_examples import _two_histograms
+    i32 = np.zeros(16, np.int32)
+    src = codegen_hip.generate(_two_histograms.ir_for(i32, i32, i32, 70001, B1=256, B2=128,
+                                                      BLOCK=1024)).source
+    assert "ek_bins0[256]" in src and "ek_bins1[128]" in src
+    assert src.count("__HIP_MEMORY_SCOPE_AGENT") == 2      # one flush per histogram

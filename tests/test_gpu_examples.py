@@ -111,6 +111,31 @@ def test_histogram(n, bins):
     assert int(got.sum()) == n
 
 
+@enceladus.jit
+def _two_histograms(x_ptr, h1_ptr, h2_ptr, n, B1: enceladus.language.constexpr,
+                    B2: enceladus.language.constexpr, BLOCK: enceladus.language.constexpr):
+    tl = enceladus.language
+    offs = tl.program_id(0) * BLOCK + tl.arange(0, BLOCK)
+    x = tl.load(x_ptr + offs, mask=offs < n, other=0)
+    a = x % B1
+    b = x // 7
+    tl.atomic_add(h1_ptr + a, 1, mask=(offs < n) & (a >= 0) & (a < B1))
+    tl.atomic_add(h2_ptr + b, 2, mask=(offs < n) & (b >= 0) & (b < B2))
+
+
+def test_two_privatised_histograms_keep_separate_bins():
+    """Two LDS-privatised atomics in one kernel: each has its own bins and its own flush
+    (bit-exact against NumPy bincount)."""
+    n, b1, b2 = 70_001, 256, 128
+    _say(f"two histograms n={n} bins={b1},{b2}")
+    x = np.random.default_rng(3).integers(0, 1000, n, dtype=np.int32)
+    h1, h2 = np.zeros(b1, np.int32), np.zeros(b2, np.int32)
+    _two_histograms[(enceladus.cdiv(n, 1024),)](x, h1, h2, n, B1=b1, B2=b2, BLOCK=1024)
+    assert np.array_equal(h1, np.bincount(x % b1, minlength=b1).astype(np.int32))
+    want2 = np.bincount(x // 7, minlength=1000)[:b2].astype(np.int32) * 2
+    assert np.array_equal(h2, want2)
+
+
 def _half(shape, seed, scale=1 / 64):
     return (np.random.default_rng(seed).standard_normal(shape, dtype=np.float32) * scale
             ).astype(np.float16)
