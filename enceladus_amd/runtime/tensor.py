@@ -70,6 +70,32 @@ class Tensor:
     def __repr__(self):
         return f"Tensor(shape={self.shape}, dtype={self.dtype})"
 
+    # ---- DLPack (reference: runtime/tensor.py:159-194, kDLMetal there) ----
+
+    def __dlpack_device__(self) -> tuple[int, int]:
+        """`(kDLROCM, 0)`: the tensor lives in HBM of GPU 0."""
+        from enceladus_amd.runtime.dlpack import K_DL_ROCM
+        return (K_DL_ROCM, 0)
+
+    def __dlpack__(self, *, stream: Any = None, max_version: tuple[int, int] | None = None,
+                   dl_device: tuple[int, int] | None = None, copy: bool | None = None):
+        """Exports the tensor as a kDLROCM DLPack capsule without copying. Pending GPU
+        work is finished first (the consumer's `stream` is then free to read it).
+
+        Raises:
+            BufferError: the consumer asked for a copy or for another device.
+        """
+        from enceladus_amd.runtime import dlpack
+        del stream
+        if copy:
+            raise BufferError("enceladus.Tensor exports without copying; copy=True isn't supported")
+        if dl_device is not None and tuple(dl_device) != (dlpack.K_DL_ROCM, 0):
+            raise BufferError(f"enceladus.Tensor lives on (kDLROCM, 0), not {tuple(dl_device)}")
+        hip.call("ek_device_sync")
+        versioned = max_version is not None and max_version[0] >= 1
+        return dlpack.export(self, self.ptr, self.shape, self.strides, self.dtype.name,
+                             versioned=versioned)
+
 
 def empty(shape, dtype=core.float32) -> Tensor:
     if isinstance(shape, int):

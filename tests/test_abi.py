@@ -60,3 +60,51 @@ def test_struct_layout_matches_header():
     from enceladus_amd.runtime import hip
     assert ctypes.sizeof(hip.DeviceInfo) == 256 + 64 + 4 * 3 + 4 + 8 * 2 + 4 * 4
     assert ctypes.sizeof(hip.FunctionAttrs) == 16
+
+
+def test_dlpack_structures_match_the_header():
+    """dlpack.h v1.0 layouts, and an unconsumed capsule releases its exporter."""
+    import ctypes
+    import gc
+    from enceladus_amd.runtime import dlpack as D
+    assert ctypes.sizeof(D.DLTensor) == 48
+    assert ctypes.sizeof(D.DLManagedTensor) == 64
+    assert ctypes.sizeof(D.DLManagedTensorVersioned) == 80
+    owner = object()
+    cap = D.export(owner, 0x1000, (3, 4), (4, 1), "bf16")
+    assert D.live_exports() == 1
+    del cap
+    gc.collect()
+    assert D.live_exports() == 0
+    cap = D.export(owner, 0x1000, (5,), (1,), "i32", versioned=True)
+    assert type(cap).__name__ == "PyCapsule"
+    del cap
+    gc.collect()
+    assert D.live_exports() == 0
+
+
+def test_hip_kernel_signature_and_packing():
+    """The raw-kernel escape hatch reads its argument types from the source and packs
+    scalars with natural alignment (no GPU needed)."""
+    import struct
+    from enceladus_amd.runtime import raw
+    src = '''
+    #include "enceladus_cdna4.h"
+    // a comment with a fake kernel(int x)
+    extern "C" __global__ void saxpy(float* __restrict__ out, const float* x,
+                                     const _Float16 *y, float a, int n, long long m,
+                                     __bf16 b, unsigned char c) { }
+    '''
+    ps = raw.parse_signature(src, "saxpy")
+    assert [p.name for p in ps] == ["out", "x", "y", "a", "n", "m", "b", "c"]
+    assert [p.pointer for p in ps] == [True, True, True, False, False, False, False, False]
+    assert [p.const for p in ps[:3]] == [False, True, True]
+    b = raw.pack(ps, [0x1000, 0x2000, 0x3000, 1.5, -3, 1 << 40, 1.0, 7])
+    assert struct.unpack_from("<QQQfiq", b, 0) == (0x1000, 0x2000, 0x3000, 1.5, -3, 1 << 40)
+    assert struct.unpack_from("<HB", b, 40) == (0x3F80, 7)     # bf16(1.0), then the byte
+    assert len(b) % 8 == 0
+    import pytest as _pt
+    with _pt.raises(ValueError):
+        raw.parse_signature(src, "nothere")
+    with _pt.raises(NotImplementedError):
+        raw.metal_kernel("kernel void k() {}", "k")

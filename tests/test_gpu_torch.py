@@ -35,3 +35,59 @@ def test_flash_attention_bf16_torch(causal, n):
     O.run_grid(attention_kernel, (n // 128, 2), q, k, v, ob, 128 ** -0.5, n, n * 128, 128,
                HEAD_DIM=128, BLOCK_M=128, BLOCK_N=64, CAUSAL=causal)
     np.testing.assert_allclose(o, ob.float().numpy(), rtol=1.6e-2, atol=1e-2)
+
+
+def test_dlpack_export_to_torch():
+    """enceladus.Tensor -> torch via DLPack (kDLROCM): shared HBM, no copy, and the
+    exporting tensor stays alive until torch releases it."""
+    import gc
+    import numpy as np
+    import torch
+    import enceladus
+    from enceladus_amd.runtime import dlpack
+    x = np.arange(12, dtype=np.float32).reshape(3, 4)
+    t = enceladus.from_numpy(x)
+    y = torch.from_dlpack(t)
+    assert y.device.type == "cuda" and tuple(y.shape) == (3, 4) and y.dtype == torch.float32
+    assert y.data_ptr() == t.data_ptr()
+    np.testing.assert_array_equal(y.cpu().numpy(), x)
+    y.mul_(2)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(t.numpy(), 2 * x)
+    del t
+    gc.collect()
+    np.testing.assert_array_equal(y.cpu().numpy(), 2 * x)   # torch still holds the memory
+    del y
+    gc.collect()
+    assert dlpack.live_exports() == 0
+
+
+_SAXPY = '''
+#include "enceladus_cdna4.h"
+extern "C" __global__ void saxpy(float* out, const float* x, const float* y, float a, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = a * x[i] + y[i];
+}
+'''
+
+
+def test_hip_kernel_escape_hatch():
+    """Hand-written HIP through enceladus.hip_kernel, with NumPy (copied, written back) and
+    torch-ROCm (device pointer) arguments. hipcc contracts a * x + y into one FMA, so the
+    expected value is the singly rounded a * x + y (exact in float64, then rounded)."""
+    import numpy as np
+    import torch
+    import enceladus
+    k = enceladus.hip_kernel(_SAXPY, "saxpy")
+    n = 10_000
+    rng = np.random.default_rng(5)
+    x, y = rng.standard_normal(n, dtype=np.float32), rng.standard_normal(n, dtype=np.float32)
+    out = np.zeros(n, np.float32)
+    k[(enceladus.cdiv(n, 256),), (256,)](out, x, y, 2.5, n)
+    want = (np.float64(2.5) * x.astype(np.float64) + y).astype(np.float32)
+    np.testing.assert_array_equal(out, want)
+    xt, yt = torch.from_numpy(x).cuda(), torch.from_numpy(y).cuda()
+    ot = torch.zeros(n, device="cuda")
+    k[enceladus.cdiv(n, 128), 128](ot, xt, yt, 2.5, n)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(ot.cpu().numpy(), want)
