@@ -139,6 +139,7 @@ class GeneratedKernel:
     lds_bytes: int
     block: int
     coarsen: int = 0       # workgroups per CU of a coarsened launch (0: one per program)
+    asserts: list = field(default_factory=list)   # tl.device_assert sites (message, loc)
 
 
 class Emitter:
@@ -163,6 +164,7 @@ class Emitter:
         self.dot_plans: dict[int, LY.DotPlan] = {}
         self.inplace: set[int] = set()
         self.extra_smem: list[tuple[str, int]] = []
+        self.asserts: list[dict] = []
 
     # ------------------------------------------------------------------ utilities
     def fresh(self, hint="v") -> str:
@@ -937,6 +939,95 @@ class Emitter:
 
     def op_barrier(self, op):
         self.emit("__syncthreads();")
+
+    # -- debugging (reference: codegen/debug.py:84-158) ------------------------------------
+    def _pid3(self) -> str:
+        if self.remap_pids or self.coarsen:
+            return "ek_pid_x, ek_pid_y, ek_pid_z"
+        return "(int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z"
+
+    def _debug_layout(self, vals) -> LY.Layout:
+        for v in vals:
+            if self.tile(v) and v.id in self.lay and self.kind.get(v.id) == "anchored":
+                return self.lay[v.id]
+        return self.default_layout(vals[0])
+
+    def op_assert(self, op):
+        """Records the first failing program in the error buffer `ek_assert_buf` (a kernel
+        argument after the runtime ones): flag, assert index, program id."""
+        idx = len(self.asserts)
+        self.asserts.append({"msg": op.attrs["msg"], "loc": op.loc})
+        cond = op.operands[0]
+        mask = op.operands[1] if len(op.operands) > 1 else None
+        call = f"ek::assert_fail(ek_assert_buf, {idx}, {self._pid3()});"
+        if not self.tile(cond):
+            c = self.name[cond.id]
+            if mask is not None:
+                c = f"({c}) || !({self.name[mask.id]})"
+            self.emit(f"if (!({c})) {call}")
+            return
+        lay = self._debug_layout([cond] + ([mask] if mask is not None else []))
+        self.prime(*[(v, lay) for v in op.operands])
+        e = self.elem(cond, lay, "r")
+        m = self.elem(mask, lay, "r") if mask is not None else None
+        ok = self.fresh("aok")
+        self.emit(f"bool {ok} = true;")
+        self.emit("#pragma unroll")
+        test = f"({e})" if m is None else f"(({e}) || !({m}))"
+        self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {ok} = {ok} && {test};")
+        self.emit(f"if (!{ok}) {call}")
+
+    _PRINTF = {"i1": ("%d", "int"), "i8": ("%d", "int"), "i16": ("%d", "int"),
+               "i32": ("%d", "int"), "u8": ("%u", "unsigned"), "u16": ("%u", "unsigned"),
+               "u32": ("%u", "unsigned"), "i64": ("%lld", "long long"),
+               "u64": ("%llu", "unsigned long long"), "fp16": ("%f", "double"),
+               "bf16": ("%f", "double"), "fp32": ("%f", "double"), "fp64": ("%f", "double")}
+
+    def op_print(self, op):
+        """printf, one line per element this thread owns (broadcast copies stay silent):
+        `pid (x, y, z) idx (i, ...) prefix values`."""
+        pre = op.attrs["prefix"].rstrip()
+        if pre:
+            pre = pre + " " if pre.endswith(":") else pre + ": "
+        pre = pre.replace("\\", "\\\\").replace('"', '\\"').replace("%", "%%")
+        convs = []
+        for v in op.operands:
+            c, cast = self._PRINTF[v.type.dtype.name]
+            if op.attrs.get("hex") and not v.type.dtype.is_floating():
+                c = "0x%llx" if v.type.dtype.itemsize == 8 else "0x%x"
+            convs.append((c, cast))
+        fmtv = " ".join(c for c, _ in convs)
+        vals = list(op.operands)
+        if not vals or not self.tile(vals[0]) or not vals[0].type.shape:
+            exprs = []
+            for v, (_, cast) in zip(vals, convs):
+                if self.tile(v):
+                    lay = self._debug_layout([v])
+                    self.prime((v, lay))
+                    x = self.elem(v, lay, "0")
+                else:
+                    x = self.name[v.id]
+                exprs.append(f"({cast})(ek::f32_or_self({x}))")
+            fmt = f"pid (%d, %d, %d) {pre}{fmtv}".rstrip()
+            args = ", ".join([self._pid3()] + exprs)
+            self.emit(f'if (ek_tid == 0) printf("{fmt}\\n", {args});')
+            return
+        lay = self._debug_layout(vals)
+        self.prime(*[(v, lay) for v in vals])
+        rank = len(lay.shape)
+        own = self.owner_cond(lay)
+        fmt = (f"pid (%d, %d, %d) idx ({', '.join(['%d'] * rank)}) {pre}{fmtv}").rstrip()
+        if own:
+            self.emit(f"if ({own}) {{")
+        self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {{")
+        coords = [self.coord(lay, d, "r") for d in range(rank)]
+        exprs = [f"({cast})(ek::f32_or_self({self.elem(v, lay, 'r')}))"
+                 for v, (_, cast) in zip(vals, convs)]
+        args = ", ".join([self._pid3()] + [f"(int)({c})" for c in coords] + exprs)
+        self.emit(f'  printf("{fmt}\\n", {args});')
+        self.emit("}")
+        if own:
+            self.emit("}")
 
     # -- memory ----------------------------------------------------------------------
     def op_load(self, op):
@@ -2578,6 +2669,9 @@ class Emitter:
             not self.coarsen
         self.gen_block(fn.body)
         kname = f"ek_{fn.name}"
+        if self.asserts:
+            params.append("uint32_t* ek_assert_buf")
+            args.append(KernelArg("ek_assert_buf", "ptr", core.uint32, "uint32_t*"))
         if self.coarsen:
             params += ["int32_t ek_np_x", "int32_t ek_np_y", "int32_t ek_np_z"]
         out = ['#include "enceladus_cdna4.h"', ""]
@@ -2677,6 +2771,7 @@ class Emitter:
         out.append("}")
         gk = GeneratedKernel(kname, "\n".join(out) + "\n", args, self.nw, self.lds, self.nt)
         gk.coarsen = int(self.coarsen)
+        gk.asserts = list(self.asserts)
         return gk
 
 

@@ -17,8 +17,27 @@ class CompilationError(Exception):
         super().__init__(text)
 
 
-class DeviceAssertionError(RuntimeError):
-    """A `tl.device_assert` that failed on the device."""
+class DeviceAssertionError(AssertionError):
+    """A `tl.device_assert` failed while a kernel ran (reference: errors.py:77-98).
+
+    Attributes:
+        message: the assert's message.
+        loc: (file, line) of the `tl.device_assert` call, or None.
+        program_id: the (x, y, z) program id of the first failing program.
+    """
+
+    def __init__(self, message: str = "", loc: tuple[str, int] | None = None,
+                 program_id: tuple[int, int, int] = (0, 0, 0)):
+        self.message = message
+        self.loc = loc
+        self.program_id = tuple(program_id)
+        super().__init__(str(self))
+
+    def __str__(self) -> str:
+        pid = ", ".join(map(str, self.program_id))
+        what = f"device assertion failed in program ({pid})"
+        text = f"{what}: {self.message}" if self.message else what
+        return f"{self.loc[0]}:{self.loc[1]}: {text}" if self.loc else text
 
 
 class HipError(RuntimeError):

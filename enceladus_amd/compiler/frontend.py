@@ -115,6 +115,9 @@ class CodeGenerator(ast.NodeVisitor):
         return CompilationError(msg, (self.filename, line), src)
 
     def visit(self, node):
+        if isinstance(node, ast.stmt):
+            # ops created for this statement carry its source location
+            self.ctx.b.loc = (self.filename, getattr(node, "lineno", 0) + self.line_offset)
         try:
             return super().visit(node)
         except CompilationError as e:

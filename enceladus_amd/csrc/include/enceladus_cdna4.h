@@ -20,6 +20,9 @@ typedef __UINT64_TYPE__ uint64_t;
 
 #define EK_INLINE __device__ __attribute__((always_inline)) inline
 
+// Device printf (tl.device_print); the HIP runtime services it through its hostcall buffer.
+extern "C" __device__ int printf(const char*, ...);
+
 namespace ek {
 
 // ---------------------------------------------------------------------------
@@ -436,6 +439,23 @@ EK_INLINE void tr_read4(T* dst, const T* src) {
       (__attribute__((address_space(3))) v4s*)(src));
   __builtin_memcpy(dst, &v, 8);
 }
+
+// tl.device_assert: the first failure claims word 0 and records the assert index and the
+// program id (words 1..4); later failures leave the record alone.
+EK_INLINE void assert_fail(uint32_t* buf, int index, int px, int py, int pz) {
+  uint32_t expected = 0;
+  if (__hip_atomic_compare_exchange_strong(buf, &expected, 1u, __ATOMIC_RELAXED,
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+    __hip_atomic_store(buf + 1, (uint32_t)index, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(buf + 2, (uint32_t)px, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(buf + 3, (uint32_t)py, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(buf + 4, (uint32_t)pz, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+// tl.device_print: 16-bit floats print through float; everything else as itself.
+template <typename T> EK_INLINE T f32_or_self(T x) { return x; }
+EK_INLINE float f32_or_self(_Float16 x) { return (float)x; }
+EK_INLINE float f32_or_self(bf16 x) { return bf16_to_f32(x); }
 
 // Buffer resource as four SGPR words, for the inline-asm copy below.
 typedef int i32x4 __attribute__((ext_vector_type(4)));

@@ -664,11 +664,35 @@ def max_contiguous(ctx, input, values):
 
 @builtin()
 def device_assert(ctx, cond, msg="", mask=None):
-    """Accepted; runtime checks are compiled out on the MI355X backend."""
+    """Checks `cond` (where `mask` is true) on the device when ENCELADUS_DEBUG=1; the first
+    failing program is reported as `DeviceAssertionError` when the launch completes. Without
+    ENCELADUS_DEBUG the check is compiled out (reference: language/ops.py:1480-1500,
+    codegen/debug.py:123-158)."""
+    if not ctx.options.get("debug"):
+        return None
+    b = ctx.b
+    c = semantic.to_value(b, cond)
+    if not c.type.dtype.is_bool():
+        c = semantic.binary(b, "ne", c, 0)
+    ops_ = [c]
+    if mask is not None:
+        m = semantic.to_value(b, mask)
+        shape = semantic.broadcast_shapes(c.type.shape, m.type.shape)
+        ops_ = [semantic.broadcast_to(b, c, shape), semantic.broadcast_to(b, m, shape)]
+    b.create("assert", ops_, [], {"msg": str(core.unwrap(msg))})
     return None
 
 
 @builtin()
 def device_print(ctx, prefix, *args, hex=False):
-    """Accepted; device printing isn't lowered on the MI355X backend."""
+    """Prints from the device with printf: one line per element a thread owns, as
+    `pid (x, y, z) idx (i, ...) prefix: values` (reference: codegen/debug.py:84-120)."""
+    b = ctx.b
+    vals = [semantic.to_value(b, a) for a in args]
+    shape = ()
+    for v in vals:
+        shape = semantic.broadcast_shapes(shape, v.type.shape)
+    vals = [semantic.broadcast_to(b, v, shape) for v in vals]
+    b.create("print", vals, [], {"prefix": str(core.unwrap(prefix)),
+                                 "hex": bool(core.unwrap(hex))})
     return None

@@ -12,6 +12,7 @@ backend: the CPU interpreter is test infrastructure here, so requesting it raise
 
 from __future__ import annotations
 
+import ctypes
 import inspect
 import os
 from dataclasses import dataclass
@@ -20,11 +21,16 @@ from typing import Any, Callable
 import numpy as np
 
 from enceladus_amd.compiler import ir
-from enceladus_amd.compiler.errors import CompilationError
+from enceladus_amd.compiler.errors import CompilationError, DeviceAssertionError
 from enceladus_amd.language import core
 from enceladus_amd.runtime import compile as C
 from enceladus_amd.runtime import device as D
 from enceladus_amd.runtime import tensor as T
+
+
+def _debug() -> bool:
+    """ENCELADUS_DEBUG=1 keeps `tl.device_assert` checks (reference: compile.py:10)."""
+    return os.environ.get("ENCELADUS_DEBUG", "") not in ("", "0")
 
 
 def cdiv(x: int, y: int) -> int:
@@ -158,12 +164,27 @@ class Launcher:
                 packed.append(v)
         if stream is None:
             stream = D.current_stream()
+        asserts = self.ck.gen.asserts
+        if asserts:
+            # ENCELADUS_DEBUG=1: the error buffer rides after the runtime arguments; the
+            # launch synchronises and reports the first failing program.
+            from enceladus_amd.runtime import hip
+            if getattr(self, "_abuf", None) is None:
+                self._abuf = T.zeros((5,), core.uint32)
+            hip.call("ek_memset", ctypes.c_void_p(self._abuf.ptr), 0, 20, None)
+            packed.append(self._abuf.ptr)
         self.ck.launch_raw(grid, self.ck.pack(packed), stream)
-        if any(b.host is not None for b in bindings):
+        if any(b.host is not None for b in bindings) or asserts:
             from enceladus_amd.runtime import hip
             hip.call("ek_device_sync")
             for b in bindings:
                 T.finish_binding(b)
+            if asserts:
+                rec = self._abuf.numpy()
+                if rec[0]:
+                    a = asserts[int(rec[1])]
+                    raise DeviceAssertionError(a["msg"], a["loc"],
+                                               (int(rec[2]), int(rec[3]), int(rec[4])))
 
 
 class JITFunction:
@@ -249,6 +270,8 @@ class JITFunction:
         for item in filter(None, os.environ.get("ENCELADUS_CODEGEN", "").split(",")):
             k, _, v = item.partition("=")
             options[k.strip()] = int(v) if v.strip().isdigit() else True
+        # ENCELADUS_DEBUG=1 keeps tl.device_assert checks (part of the key below)
+        options["debug"] = _debug()
         fn_ir = C.build_module(self, types, facts, consts, num_warps, options)
         ck = C.compile_ir(fn_ir, options)
         runtime_names = list(types.keys())
@@ -258,7 +281,7 @@ class JITFunction:
         types, facts, consts = self.specialize(vals)
         key = (self._key(types, facts, consts, num_warps, dot_warps),
                os.environ.get("ENCELADUS_CODEGEN", ""),
-               os.environ.get("ENCELADUS_OVERRIDE_DIR", ""))
+               os.environ.get("ENCELADUS_OVERRIDE_DIR", ""), _debug())
         lc = self._cache.get(key)
         if lc is None:
             lc = self._compile_for(types, facts, consts, num_warps, dot_warps)
@@ -294,7 +317,8 @@ class JITFunction:
         vals = self._bind(args, kwargs)
         types, facts, consts = self.specialize(vals)
         return C.build_module(self, types, facts, consts, num_warps,
-                              {"dot_warps": tuple(dot_warps) if dot_warps else None})
+                              {"dot_warps": tuple(dot_warps) if dot_warps else None,
+                               "debug": _debug()})
 
     def explain(self, *args, **kwargs) -> str:
         ck = self.warmup(*args, **kwargs)

@@ -37,3 +37,34 @@ def test_override_dir_replaces_the_generated_source(monkeypatch, tmp_path):
     # a directory without a file of the kernel's name leaves the generated source alone
     ck3 = _compile(monkeypatch, tmp_path, ENCELADUS_OVERRIDE_DIR=str(tmp_path))
     assert ck3.hip == ck.hip
+
+
+def _debug_kernel():
+    import enceladus
+    import enceladus.language as tl
+
+    @enceladus.jit
+    def checked(x_ptr, n, BLOCK: tl.constexpr):
+        offs = tl.program_id(0) * BLOCK + tl.arange(0, BLOCK)
+        x = tl.load(x_ptr + offs, mask=offs < n, other=0.0)
+        tl.device_assert(x < 100.0, "x must stay below 100", mask=offs < n)
+        tl.device_print("x", x)
+    return checked
+
+
+def test_device_assert_is_compiled_only_with_debug(monkeypatch, tmp_path):
+    """ENCELADUS_DEBUG=1 keeps tl.device_assert (an error-buffer argument after the runtime
+    arguments); without it the check is compiled out. tl.device_print always lowers to
+    printf (reference: codegen/debug.py:84-158, compile.py:10)."""
+    monkeypatch.setenv("ENCELADUS_CACHE_DIR", str(tmp_path))
+    k = _debug_kernel()
+    x = np.zeros(16, np.float32)
+    monkeypatch.setenv("ENCELADUS_DEBUG", "1")
+    ck = C.compile_ir(k.ir_for(x, 100, BLOCK=64))
+    assert "ek::assert_fail(ek_assert_buf, 0" in ck.hip and "printf(" in ck.hip
+    assert [a.name for a in ck.args] == ["x_ptr", "n", "ek_assert_buf"]
+    assert ck.gen.asserts[0]["msg"] == "x must stay below 100"
+    monkeypatch.setenv("ENCELADUS_DEBUG", "0")
+    ck2 = C.compile_ir(k.ir_for(x, 100, BLOCK=64))
+    assert "assert_fail" not in ck2.hip and "printf(" in ck2.hip
+    assert [a.name for a in ck2.args] == ["x_ptr", "n"]

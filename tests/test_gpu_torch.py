@@ -91,3 +91,36 @@ def test_hip_kernel_escape_hatch():
     k[enceladus.cdiv(n, 128), 128](ot, xt, yt, 2.5, n)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(ot.cpu().numpy(), want)
+
+
+def test_device_assert_reports_the_failing_program(monkeypatch):
+    """ENCELADUS_DEBUG=1: a failing tl.device_assert raises DeviceAssertionError naming the
+    first failing program and the assert's message and line; a passing one doesn't."""
+    import numpy as np
+    import pytest as _pt
+    import enceladus
+    from tests.test_compile_env import _debug_kernel
+    monkeypatch.setenv("ENCELADUS_DEBUG", "1")
+    k = _debug_kernel()
+    x = np.zeros(1000, np.float32)
+    k[(enceladus.cdiv(1000, 64),)](x, 1000, BLOCK=64)          # all below 100: no error
+    x[700] = 500.0                                             # program 700 // 64 = 10
+    with _pt.raises(enceladus.DeviceAssertionError) as e:
+        k[(enceladus.cdiv(1000, 64),)](x, 1000, BLOCK=64)
+    assert e.value.program_id == (10, 0, 0)
+    assert "x must stay below 100" in str(e.value) and e.value.loc[1] > 0
+
+
+def test_device_print_lines(capfd):
+    """tl.device_print: one printf line per owned element, prefixed with the program id."""
+    import numpy as np
+    import enceladus
+    from tests.test_compile_env import _debug_kernel
+    k = _debug_kernel()
+    x = np.arange(8, dtype=np.float32)
+    k[(1,)](x, 8, BLOCK=64)
+    enceladus.synchronize()
+    out = capfd.readouterr().out
+    lines = [ln for ln in out.splitlines() if ln.startswith("pid (0, 0, 0) idx")]
+    assert len(lines) == 64
+    assert "pid (0, 0, 0) idx (3) x: 3.000000" in lines
