@@ -347,7 +347,7 @@ def main():
         ATTN_CONFIGS = [tuple(int(x) for x in args.attn.split(","))]
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; multi-GPU runs are out "
-                          "of scope (every config shards with no exchange; see DESIGN.md)"}))
+                          "of scope (every config shards with no exchange between GPUs)"}))
         sys.exit(2)
     import torch
     torch.cuda.init()

@@ -165,6 +165,7 @@ class Emitter:
         self.inplace: set[int] = set()
         self.extra_smem: list[tuple[str, int]] = []
         self.asserts: list[dict] = []
+        self.split_bit: dict[int, int] = {}
 
     # ------------------------------------------------------------------ utilities
     def fresh(self, hint="v") -> str:
@@ -221,6 +222,22 @@ class Emitter:
             return 1
         v = min(1 << nb, info.contig[d], max(1, info.div[d] // es), max(1, 16 // es))
         return 1 << LY.log2(max(1, v))
+
+    def wave_run_bytes(self, ptr: ir.Value, lay: LY.Layout) -> int:
+        """Bytes one vector access of `ptr` in `lay` covers contiguously across a wave:
+        the register vector, then the lane bits that continue the same dim."""
+        info = self.axis.get(ptr)
+        d, nb = lay.vec_dim_bits()
+        if nb == 0 and lay.lane and lay.lane[0] is not None:
+            d = lay.lane[0][0]
+        v = self.mem_vec(ptr, lay)
+        run = v
+        if v >= (1 << nb):
+            k = 0
+            while k < len(lay.lane) and lay.lane[k] == (d, nb + k):
+                k += 1
+            run = v << k
+        return min(run, info.contig[d]) * ptr.type.dtype.itemsize
 
     def lay_of(self, v: ir.Value):
         return self.lay.get(v.id)
@@ -347,7 +364,7 @@ class Emitter:
             return
         if n in ("const", "arange", "splat"):
             self.kind[res.id] = "cheap"
-        elif n in ("broadcast", "expand_dims", "trans", "hint"):
+        elif n in ("broadcast", "expand_dims", "trans", "hint", "reshape"):
             src = op.operands[0]
             if not self._anch(src):
                 self.kind[res.id] = "cheap"
@@ -360,8 +377,44 @@ class Emitter:
                     self.lay[res.id] = sl.expand(op.attrs["axis"])
                 elif n == "trans":
                     self.lay[res.id] = sl.permute(op.attrs["perm"])
+                elif n == "reshape":
+                    self.lay[res.id] = sl.reshape(res.type.shape)
                 else:
                     self.lay[res.id] = sl
+        elif n == "join":
+            # the new last dim is register bit 0: res[2r + k] = (a, b)[k][r]
+            self.kind[res.id] = "anchored"
+            base = next((self.lay[o.id] for o in op.operands
+                         if self._anch(o) and self.kind[o.id] == "anchored"), None)
+            base = base or self.default_layout(op.operands[0])
+            rank = len(base.shape)
+            self.lay[res.id] = LY.Layout(res.type.shape, ((rank, 0),) + tuple(base.reg),
+                                         base.lane, base.warp)
+        elif n == "split":
+            x = op.operands[0]
+            rank = len(x.type.shape)
+            xl = self.lay[x.id] if self._anch(x) else None
+            bit = (rank - 1, 0)
+            if xl is not None and (bit in xl.reg or bit in xl.lane):
+                # a register bit selects registers; a lane bit becomes two shuffles, and
+                # both halves are then replicated over that lane bit
+                mode = ("reg", xl.reg.index(bit)) if bit in xl.reg else \
+                    ("lane", xl.lane.index(bit))
+                out = LY.Layout(res.type.shape, tuple(b for b in xl.reg if b != bit),
+                                tuple(None if b == bit else b for b in xl.lane),
+                                tuple(None if b == bit else b for b in xl.warp))
+            else:
+                out = self.default_layout(res)
+                mode = ("reg", 0)
+            for r in op.results:
+                self.kind[r.id] = "anchored"
+                self.lay[r.id] = out
+            self.split_bit[res.id] = mode
+        elif n == "shift":
+            src = op.operands[0]
+            self.kind[res.id] = "anchored"
+            self.lay[res.id] = self.lay_of(src) if self._anch(src) and \
+                self.kind[src.id] == "anchored" else self.default_layout(res)
         elif n in ("binary", "unary", "cast", "select", "fma", "ptr_add", "bitcast"):
             anch = [o for o in op.operands if self.tile(o) and self._anch(o)]
             if not anch:
@@ -419,9 +472,6 @@ class Emitter:
                 idx = op.operands[0].op.operands[1]
                 if self._anch(idx) and self.lay[idx.id].shape == res.type.shape:
                     self.lay[res.id] = self.lay[idx.id]
-        elif n == "reshape":
-            self.kind[res.id] = "anchored"
-            self.lay[res.id] = self.default_layout(res)
         else:
             raise CompilationError(f"the HIP backend doesn't lower `{n}`")
 
@@ -651,6 +701,19 @@ class Emitter:
             return self.cheap(op.operands[0], xc)
         if n == "hint":
             return self.cheap(op.operands[0], coords)
+        if n == "reshape":
+            # row-major linear index, then the source coordinates (power-of-two dims)
+            shp, src = v.type.shape, op.operands[0]
+            lin, sh = [], 0
+            for d in reversed(range(len(shp))):
+                lin.append(f"(({coords[d]}) << {sh})" if sh else f"({coords[d]})")
+                sh += LY.log2(shp[d])
+            le = "(" + " | ".join(lin) + ")" if lin else "0"
+            xc, sh = [None] * len(src.type.shape), 0
+            for d in reversed(range(len(src.type.shape))):
+                xc[d] = f"(({le} >> {sh}) & {src.type.shape[d] - 1})"
+                sh += LY.log2(src.type.shape[d])
+            return self.cheap(src, xc)
         xs = []
         for o in op.operands:
             xs.append(self.name[o.id] if not self.tile(o) else self.cheap(o, coords))
@@ -676,6 +739,8 @@ class Emitter:
                 for i, p in enumerate(perm):
                     inv[p] = i
                 lay = lay.permute(tuple(inv))
+            elif op.name == "reshape":
+                lay = lay.reshape(src.type.shape)
             v = src
         return v, lay, r
 
@@ -869,7 +934,8 @@ class Emitter:
         if n in ("binary", "unary", "cast", "select", "fma", "ptr_add", "bitcast"):
             self.op_elementwise(op)
             return
-        if n in ("const", "arange", "splat", "broadcast", "expand_dims", "trans", "hint"):
+        if n in ("const", "arange", "splat", "broadcast", "expand_dims", "trans", "hint",
+                 "reshape"):
             res = op.result
             k = self.kind.get(res.id)
             if k == "scalar":
@@ -1117,7 +1183,11 @@ class Emitter:
         if self._anch(val) and self.kind[val.id] == "anchored":
             vl = self.lay[val.id]
             want = self.mem_vec(ptr, lay)
-            if vl.shape == lay.shape and self.mem_vec(ptr, vl) >= want:
+            # keep the value where it is when that stores as wide a vector, or when each
+            # store instruction still writes one contiguous 256-byte run per wave: either
+            # beats a round trip through LDS
+            if vl.shape == lay.shape and (self.mem_vec(ptr, vl) >= want or
+                                          self.wave_run_bytes(ptr, vl) >= 256):
                 lay = vl
         V = self.mem_vec(ptr, lay)
         own = self.owner_cond(lay)
@@ -1502,32 +1572,83 @@ class Emitter:
         self.emit("}")
         self.define(res, nm)
 
-    # -- reshape ----------------------------------------------------------------------
-    def op_reshape(self, op):
-        src, res = op.operands[0], op.result
-        t = ctype(res.type.dtype)
-        es = res.type.dtype.itemsize
-        sl = self.lay[src.id] if self._anch(src) else self.default_layout(src)
-        arr = self.array(src, sl)
-        dst = self.lay[res.id]
-        n = res.type.numel
-        self.need_lds(n * es)
+    # -- join / split (reference: language/ops.py:832-902, codegen/msl.py:693-747) --------
+    def op_join(self, op):
+        res = op.result
+        lay = self.lay[res.id]
+        base = LY.Layout(op.operands[0].type.shape, tuple(lay.reg[1:]), lay.lane, lay.warp)
+        a, b = (self.array(o, base) for o in op.operands)
+        nm = self.fresh("jn")
+        self.emit(f"{ctype(res.type.dtype)} {nm}[{lay.nregs}];")
+        self.emit("#pragma unroll")
+        self.emit(f"for (int r = 0; r < {base.nregs}; ++r) {{ {nm}[2 * r] = {a}[r]; "
+                  f"{nm}[2 * r + 1] = {b}[r]; }}")
+        self.define(res, nm)
 
-        def lin(lay, r):
-            terms = []
-            s = 1
-            for d in reversed(range(len(lay.shape))):
-                terms.append(f"({self.coord(lay, d, r)}) * {s}")
-                s *= lay.shape[d]
-            return " + ".join(terms)
-        nm = self.fresh("rs")
-        self.emit(f"{t} {nm}[{dst.nregs}];")
+    def op_split(self, op):
+        x = op.operands[0]
+        out = self.lay[op.results[0].id]
+        mode, k = self.split_bit[op.results[0].id]
+        bit = (len(x.type.shape) - 1, 0)
+        t = ctype(x.type.dtype)
+        if mode == "lane":
+            lane = list(out.lane)
+            lane[k] = bit
+            xa = self.array(x, LY.Layout(x.type.shape, out.reg, tuple(lane), out.warp))
+            for half, r_ in enumerate(op.results):
+                src = f"(ek_lane | {1 << k})" if half else f"(ek_lane & ~{1 << k})"
+                nm = self.fresh("sp")
+                self.emit(f"{t} {nm}[{out.nregs}];")
+                self.emit("#pragma unroll")
+                self.emit(f"for (int r = 0; r < {out.nregs}; ++r) {nm}[r] = "
+                          f"ek::shfl({xa}[r], {src});")
+                self.define(r_, nm)
+            return
+        regs = list(out.reg)
+        regs.insert(k, bit)
+        xl = LY.Layout(x.type.shape, tuple(regs), out.lane, out.warp)
+        xa = self.array(x, xl)
+        lo = f"(r & {(1 << k) - 1})" if k else "0"
+        for half, r_ in enumerate(op.results):
+            nm = self.fresh("sp")
+            self.emit(f"{t} {nm}[{out.nregs}];")
+            self.emit("#pragma unroll")
+            self.emit(f"for (int r = 0; r < {out.nregs}; ++r) {nm}[r] = "
+                      f"{xa}[((r >> {k}) << {k + 1}) | ({half} << {k}) | {lo}];")
+            self.define(r_, nm)
+
+    # -- shift along an axis (the Hillis-Steele steps of tl.associative_scan) ------------
+    def op_shift(self, op):
+        """res[..., i, ...] = x[..., i - by, ...] where that is in range, else x itself,
+        through one LDS round trip (the tile is written row-major, then read shifted)."""
+        x, res = op.operands[0], op.result
+        ax, by = op.attrs["axis"], op.attrs["by"]
+        lay = self.lay[res.id]
+        xa = self.array(x, lay)
+        t = ctype(x.type.dtype)
+        shp = x.type.shape
+        self.need_lds(x.type.numel * max(4, x.type.dtype.itemsize))
+        strides, st = [0] * len(shp), 1
+        for d in reversed(range(len(shp))):
+            strides[d] = st
+            st *= shp[d]
+        cs = [self.coord(lay, d, "r") for d in range(len(shp))]
+        lin = " + ".join(f"({c}) * {strides[d]}" for d, c in enumerate(cs))
+        lin_src = " + ".join(f"({c if d != ax else 'c'}) * {strides[d]}"
+                             for d, c in enumerate(cs))
+        nm = self.fresh("sh")
+        self.emit(f"{t} {nm}[{lay.nregs}];")
         self.emit("{")
         self.emit(f"  {t}* sm = reinterpret_cast<{t}*>(ek_smem);")
         self.emit("  __syncthreads();")
-        self.emit(f"  for (int r = 0; r < {sl.nregs}; ++r) sm[{lin(sl, 'r')}] = {arr}[r];")
+        self.emit("  #pragma unroll")
+        self.emit(f"  for (int r = 0; r < {lay.nregs}; ++r) sm[{lin}] = {xa}[r];")
         self.emit("  __syncthreads();")
-        self.emit(f"  for (int r = 0; r < {dst.nregs}; ++r) {nm}[r] = sm[{lin(dst, 'r')}];")
+        self.emit("  #pragma unroll")
+        self.emit(f"  for (int r = 0; r < {lay.nregs}; ++r) {{")
+        self.emit(f"    int c = (int)({cs[ax]}) - ({by});")
+        self.emit(f"    {nm}[r] = (c >= 0 && c < {shp[ax]}) ? sm[{lin_src}] : {xa}[r];")
+        self.emit("  }")
         self.emit("}")
         self.define(res, nm)
 
@@ -1546,7 +1667,9 @@ class Emitter:
         acc_t = "float" if is_half(dt) else ctype(dt)
         arg = kind in ("argmax", "argmin")
         comb = {"sum": "ek::Sum", "max": "ek::Max", "min": "ek::Min",
-                "argmax": "ek::Max", "argmin": "ek::Min"}[kind]
+                "argmax": "ek::Max", "argmin": "ek::Min", "first": "ek::First"}[kind]
+        if kind == "first" and src.type.shape[ax] != 1:
+            raise CompilationError("internal: reduce kind `first` takes a size-1 axis")
         axis_reg = [i for i, b in enumerate(sl.reg) if b[0] == ax]
         keep_reg = [i for i, b in enumerate(sl.reg) if b[0] != ax]
         ro_n = 1 << len(keep_reg)

@@ -595,21 +595,38 @@ class CodeGenerator(ast.NodeVisitor):
                    **{k: core.unwrap(v) for k, v in kwargs.items()})
 
     def inline(self, jfn, args, kwargs, node):
-        fn = jfn.fn
-        sig = inspect.signature(fn)
         try:
-            bound = sig.bind(*args, **kwargs)
-        except TypeError as e:
-            raise self.error(node, f"bad call to `{fn.__name__}`: {e}") from None
-        bound.apply_defaults()
-        scope = dict(bound.arguments)
-        tree, fname, off, lines = parse_function(fn)
-        gen = CodeGenerator(self.ctx, fn, scope, fname, off, lines)
-        try:
-            gen.visit_stmts(tree.body)
-        except _Return as r:
-            return r.value
-        return None
+            return inline_jit(self.ctx, jfn, args, kwargs)
+        except _BadCall as e:
+            raise self.error(node, str(e)) from None
+
+
+class _BadCall(Exception):
+    pass
+
+
+def inline_jit(ctx: Context, jfn, args, kwargs=None):
+    """Emits the body of the @jit function `jfn` called with `args` at the builder's
+    current position and returns its return value (a tuple for several values)."""
+    fn = jfn.fn
+    sig = inspect.signature(fn)
+    try:
+        bound = sig.bind(*args, **(kwargs or {}))
+    except TypeError as e:
+        raise _BadCall(f"bad call to `{fn.__name__}`: {e}") from None
+    bound.apply_defaults()
+    scope = dict(bound.arguments)
+    tree, fname, off, lines = parse_function(fn)
+    gen = CodeGenerator(ctx, fn, scope, fname, off, lines)
+    try:
+        gen.visit_stmts(tree.body)
+    except _Return as r:
+        return r.value
+    return None
+
+
+def is_jit(obj: Any) -> bool:
+    return _is_jit(obj)
 
 
 class _BreakScan(Exception):

@@ -129,6 +129,20 @@ class Layout:
         shape = tuple(self.shape[p] for p in perm)
         return self._map(lambda b: (inv[b[0]], b[1]), shape)
 
+    def reshape(self, shape: tuple[int, ...]) -> "Layout":
+        """The same hardware bits over a row-major reshape of the tile: with power-of-two
+        dims a reshape only relabels coordinate bits (linear bit position is preserved)."""
+        def table(shp):
+            pos, out = 0, {}
+            for d in reversed(range(len(shp))):
+                for i in range(log2(shp[d])):
+                    out[(d, i)] = pos + i
+                pos += log2(shp[d])
+            return out
+        src = table(self.shape)
+        back = {p: b for b, p in table(tuple(shape)).items()}
+        return self._map(lambda b: back[src[b]], shape)
+
     def project(self, shape: tuple[int, ...]) -> "Layout":
         """Restricts to a broadcast source shape: bits of size-1 dims become broadcast."""
         def f(b):

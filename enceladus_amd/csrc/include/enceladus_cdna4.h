@@ -259,6 +259,10 @@ template <int MASK, typename T> EK_INLINE T shfl_xor(T v) {
 struct Sum {
   template <typename T> static EK_INLINE T op(T a, T b) { return a + b; }
 };
+// Keeps the first operand: the element of a size-1 axis (split of a (2,) tile).
+struct First {
+  template <typename T> static EK_INLINE T op(T a, T) { return a; }
+};
 struct Max {
   template <typename T> static EK_INLINE T op(T a, T b) {
     if constexpr (__is_same(T, float)) return __builtin_fmaxf(a, b);

@@ -9,18 +9,19 @@ from enceladus_amd.language.core import (  # noqa: F401
     uint16, uint32, uint64,
 )
 from enceladus_amd.language.ops import (  # noqa: F401
-    arange, argmax, argmin, atomic_add, atomic_and, atomic_cas, atomic_max, atomic_min,
+    arange, argmax, argmin, associative_scan, atomic_add, atomic_and, atomic_cas, atomic_max, atomic_min,
     atomic_or, atomic_xchg, atomic_xor, broadcast_to, cast, cdiv, ceil, clamp, cos, cumsum,
     debug_barrier, device_assert, device_print, dot, erf, exp, exp2, expand_dims, floor, fma,
-    full, full_like, load, log, log2, make_tensor_descriptor, max_contiguous, maximum,
+    full, full_like, join, load, log, log2, make_tensor_descriptor, max_contiguous, maximum,
     minimum, multiple_of, num_programs, permute, program_id, reshape, rsqrt, sigmoid, sin,
-    sqrt, static_assert, static_print, static_range, store, tanh, trans, where, zeros,
+    split, sqrt, static_assert, static_print, static_range, store, tanh, trans, where, zeros,
     zeros_like,
 )
 from enceladus_amd.language.ops import abs_ as abs  # noqa: F401
 from enceladus_amd.language.ops import max_ as max  # noqa: F401
 from enceladus_amd.language.ops import min_ as min  # noqa: F401
 from enceladus_amd.language.ops import range  # noqa: F401
+from enceladus_amd.language.ops import reduce_ as reduce  # noqa: F401
 from enceladus_amd.language.ops import sum_ as sum  # noqa: F401
 
 

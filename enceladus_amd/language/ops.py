@@ -1,10 +1,10 @@
 """The `tl` builtins: each one builds IR when a kernel is compiled.
 
 Calling a builtin outside a kernel raises. Signatures and semantics follow the reference
-language (reference: src/enceladus/language/ops.py; op index in SURVEY-listed lines
-136-2074: program_id :141, arange :179, full :203, load :305, store :365,
+language (reference: src/enceladus/language/ops.py, lines 136-2074: program_id :141, arange :179, full :203, load :305, store :365,
 make_tensor_descriptor :437, where :557, to :668, sum :983, max :1015, dot :1244,
-atomic_add :1943, cumsum :2064).
+atomic_add :1943, cumsum :2064, join :840, split :875, reduce :1100,
+associative_scan :2097).
 """
 
 from __future__ import annotations
@@ -496,6 +496,230 @@ def cumsum(ctx, input, axis=0, reverse=False, dtype=None):
 
 F.TILE_METHODS["cumsum"] = lambda ctx, x, axis=0, reverse=False: cumsum._ek_frontend(
     ctx, x, axis, reverse)
+
+
+# -- join / split (reference: language/ops.py:815-902) -------------------------------
+
+def _no_pointers(fname: str, *xs) -> None:
+    for x in xs:
+        if isinstance(x, ir.Value) and x.type.ptr:
+            raise CompilationError(
+                f"tl.{fname} doesn't support tiles of pointers. Apply it to the integer "
+                "offsets instead, and add the result to the base pointer.")
+
+
+def _join_dtype(a, b) -> core.dtype:
+    """A Python number takes the other operand's dtype; two runtime operands must already
+    share one (as in `tl.where` for literals, as in Triton for the rest)."""
+    dt = semantic.computation_dtype("select", a, b)
+    for x, other in ((a, b), (b, a)):
+        if isinstance(x, core.dtype) and x is not dt:
+            what = f"the literal {other!r}" if semantic.is_literal(other) else str(other)
+            raise CompilationError(f"tl.join needs two operands of one dtype, but got {x} and "
+                                   f"{what}. Convert one operand with `.to(dtype)` first.")
+    return dt
+
+
+def _first(b: ir.Builder, v: ir.Value) -> ir.Value:
+    """The only element of a tile of shape (1,), as a scalar."""
+    return b.create("reduce", [v], [ir.TType((), v.type.dtype)],
+                    {"axis": 0, "kind": "first"}).result
+
+
+@builtin()
+def join(ctx, a, b):
+    """Joins `a` and `b` along a new last dimension of size 2: the operands broadcast to
+    one shape S and the result has shape (*S, 2), `[..., 0]` from `a` and `[..., 1]` from
+    `b`. Two scalars give a tile of shape (2,)."""
+    x, y = core.unwrap(a), core.unwrap(b)
+    _no_pointers("join", x, y)
+    bld = ctx.b
+    dt = _join_dtype(semantic.dtype_of(x), semantic.dtype_of(y))
+    xv, yv = semantic.to_value(bld, x, dt), semantic.to_value(bld, y, dt)
+    shape = semantic.broadcast_shapes(xv.type.shape, yv.type.shape)
+    scalar = not shape
+    shape = shape or (1,)
+    xv, yv = (semantic.broadcast_to(bld, v, shape) for v in (xv, yv))
+    out = bld.create("join", [xv, yv], [ir.TType((*shape, 2), dt)]).result
+    if scalar:
+        out = bld.create("reshape", [out], [out.type.with_shape((2,))]).result
+    return out
+
+
+@builtin()
+def split(ctx, a):
+    """Splits `a` along its last dimension, which must be 2: returns (a[..., 0],
+    a[..., 1]), the inverse of `tl.join`. A tile of shape (2,) gives two scalars."""
+    v = _tile(ctx, a, "split")
+    _no_pointers("split", v)
+    shp = v.type.shape
+    if not shp or shp[-1] != 2:
+        raise CompilationError(
+            f"tl.split needs a tile whose last dimension is 2, but got a tile of shape {shp}. "
+            "Reshape the tile first so that its last dimension is 2.")
+    b = ctx.b
+    rank1 = len(shp) == 1
+    if rank1:
+        v = b.create("reshape", [v], [v.type.with_shape((1, 2))]).result
+    t = v.type.with_shape(v.type.shape[:-1])
+    outs = b.create("split", [v], [t, t]).results
+    if rank1:
+        outs = [_first(b, r) for r in outs]
+    return outs[0], outs[1]
+
+
+# -- reductions and scans with a combine function ---------------------------------------
+# Both are lowered here to tile ops the backend already has, in the combination order of
+# the reference interpreter: `tl.reduce` halves the axis (combine(x[:h], x[h:]), reference
+# ops.py:1061-1096) and `tl.associative_scan` is Hillis-Steele (combine(x[i-s], x[i]) for
+# s = 1, 2, 4, ..., reference ops.py:2026-2044), so results match it bit for bit.
+
+def _combine_fn(fn, fname: str):
+    fn = core.unwrap(fn)
+    if not F.is_jit(fn):
+        raise CompilationError(
+            f"tl.{fname} needs a @enceladus.jit function as `combine_fn`. Plain Python "
+            "functions aren't accepted, because the kernel cache doesn't track their source.")
+    return fn
+
+
+def _combine(ctx, fn, lhs: list, rhs: list, fname: str) -> list:
+    b = ctx.b
+    res = F.inline_jit(ctx, fn, [*lhs, *rhs])
+    res = list(res) if isinstance(res, tuple) else [res]
+    if len(res) != len(lhs):
+        raise CompilationError(f"combine_fn returns {len(res)} values for {len(lhs)} inputs. "
+                               "Return one value per input.")
+    out = []
+    for i, (r, x) in enumerate(zip(res, lhs)):
+        r = core.unwrap(r)
+        dt, shape = x.type.dtype, x.type.shape
+        if isinstance(r, ir.Value):
+            if r.type.dtype is not dt or r.type.ptr:
+                raise CompilationError(
+                    f"result {i} of combine_fn has dtype {r.type.dtype}, but {dt} is expected "
+                    "here. Convert it with `.to(...)`.")
+        elif semantic.is_literal(r):
+            if isinstance(r, float) and not dt.is_floating():
+                raise CompilationError(f"result {i} of combine_fn is the float {r!r}, but the "
+                                       f"input is {dt}")
+            r = semantic.to_value(b, r, dt)
+        else:
+            raise CompilationError(f"result {i} of combine_fn isn't a value: {r!r}")
+        out.append(semantic.broadcast_to(b, r, shape))
+    return out
+
+
+def _halves(b: ir.Builder, v: ir.Value, ax: int) -> tuple[ir.Value, ir.Value]:
+    """(v[..., :n/2, ...], v[..., n/2:, ...]) along `ax`, as views plus one split."""
+    shp = v.type.shape
+    h = shp[ax] // 2
+    s2 = shp[:ax] + (2, h) + shp[ax + 1:]
+    v = b.create("reshape", [v], [v.type.with_shape(s2)]).result
+    perm = tuple(d for d in _bi.range(len(s2)) if d != ax) + (ax,)
+    v = b.create("trans", [v], [v.type.with_shape(tuple(s2[p] for p in perm))],
+                 {"perm": perm}).result
+    t = v.type.with_shape(v.type.shape[:-1])
+    lo, hi = b.create("split", [v], [t, t]).results
+    return lo, hi
+
+
+@builtin(name="reduce")
+def reduce_(ctx, input, axis, combine_fn, keep_dims=False):
+    """Reduces `input` (a tile, or a tuple of tiles of one shape) along `axis` (all of it
+    for None) with `combine_fn(a0, ..., b0, ...)`, a @enceladus.jit function that must be
+    associative and commutative."""
+    b = ctx.b
+    fn = _combine_fn(combine_fn, "reduce")
+    single = not isinstance(core.unwrap(input), tuple)
+    vals = [_tile(ctx, x, "reduce") for x in ((input,) if single else core.unwrap(input))]
+    _no_pointers("reduce", *vals)
+    if len({v.type.shape for v in vals}) != 1:
+        raise CompilationError("tl.reduce needs inputs of one shape, but got "
+                               f"{sorted({v.type.shape for v in vals})}")
+    rank = len(vals[0].type.shape)
+    if rank == 0:
+        return vals[0] if single else tuple(vals)
+    axis = core.unwrap(axis)
+    if axis is None:
+        vals = [b.create("reshape", [v], [v.type.with_shape((v.type.numel,))]).result
+                if rank > 1 else v for v in vals]
+        ax = 0
+    else:
+        ax = _axis(axis, rank)
+    while vals[0].type.shape[ax] > 1:
+        parts = [_halves(b, v, ax) for v in vals]
+        vals = _combine(ctx, fn, [p[0] for p in parts], [p[1] for p in parts], "reduce")
+    shp = list(vals[0].type.shape)
+    del shp[ax]
+    if shp:
+        outs = [b.create("reshape", [v], [v.type.with_shape(tuple(shp))]).result for v in vals]
+    else:
+        outs = [_first(b, v) for v in vals]
+    if core.unwrap(keep_dims):
+        if axis is None:
+            outs = [semantic.broadcast_to(b, r, (1,) * rank) for r in outs]
+        else:
+            outs = [semantic.expand_dims(b, r, ax) for r in outs]
+    return outs[0] if single else tuple(outs)
+
+
+F.TILE_METHODS["reduce"] = lambda ctx, x, axis, combine_fn, keep_dims=False: \
+    reduce_._ek_frontend(ctx, x, axis, combine_fn, keep_dims)
+
+
+@builtin()
+def associative_scan(ctx, input, axis, combine_fn, reverse=False):
+    """The inclusive scan of `input` (a tile, or a tuple of tiles of one shape) along
+    `axis` with `combine_fn(a0, ..., b0, ...)`, where the `a` values come from earlier
+    elements (later ones with `reverse=True`). It must be associative; it need not be
+    commutative."""
+    b = ctx.b
+    fn = _combine_fn(combine_fn, "associative_scan")
+    single = not isinstance(core.unwrap(input), tuple)
+    vals = [_tile(ctx, x, "associative_scan")
+            for x in ((input,) if single else core.unwrap(input))]
+    _no_pointers("associative_scan", *vals)
+    if len({v.type.shape for v in vals}) != 1:
+        raise CompilationError("tl.associative_scan needs inputs of one shape, but got "
+                               f"{sorted({v.type.shape for v in vals})}")
+    shp = vals[0].type.shape
+    if not shp:
+        raise CompilationError("tl.associative_scan needs a tile")
+    if core.unwrap(axis) is None:
+        raise CompilationError("tl.associative_scan needs an `axis`, for example `axis=0`")
+    ax = _axis(axis, len(shp))
+    rev = core.unwrap(reverse)
+    if not isinstance(rev, bool):
+        raise CompilationError(f"`reverse` must be a compile-time bool, but got {rev!r}")
+    n = shp[ax]
+    idx = None
+    s = 1
+    while s < n:
+        if idx is None:
+            idx = b.create("arange", [], [ir.TType((n,), core.int32)], {"start": 0}).result
+            for _ in _bi.range(ax):
+                idx = semantic.expand_dims(b, idx, 0)
+            for _ in _bi.range(len(shp) - ax - 1):
+                idx = semantic.expand_dims(b, idx, len(idx.type.shape))
+        by = -s if rev else s
+        prev = [b.create("shift", [v], [v.type], {"axis": ax, "by": by}).result for v in vals]
+        comb = _combine(ctx, fn, prev, vals, "associative_scan")
+        keep = semantic.binary(b, "lt", idx, n - s) if rev else semantic.binary(b, "ge", idx, s)
+        vals = [semantic.select(b, keep, c, v) for c, v in zip(comb, vals)]
+        s *= 2
+    return vals[0] if single else tuple(vals)
+
+
+F.TILE_METHODS["associative_scan"] = lambda ctx, x, axis, combine_fn, reverse=False: \
+    associative_scan._ek_frontend(ctx, x, axis, combine_fn, reverse)
+F.TILE_METHODS["join"] = lambda ctx, x, other: join._ek_frontend(ctx, x, other)
+F.TILE_METHODS["split"] = lambda ctx, x: split._ek_frontend(ctx, x)
+F.TILE_METHODS["reshape"] = lambda ctx, x, *shape, can_reorder=False: reshape._ek_frontend(
+    ctx, x, *shape, can_reorder=can_reorder)
+F.TILE_METHODS["broadcast_to"] = lambda ctx, x, *shape: broadcast_to._ek_frontend(
+    ctx, x, *shape)
+F.TILE_METHODS["expand_dims"] = lambda ctx, x, axis: expand_dims._ek_frontend(ctx, x, axis)
 
 
 # -- dot ----------------------------------------------------------------------------

@@ -5,6 +5,8 @@ reference's compile-without-GPU checks (reference tests/conftest.py:18-20, jit.p
 import numpy as np
 import pytest
 
+import enceladus
+import enceladus.language as tl
 from enceladus_amd.compiler import codegen_hip, ir
 from enceladus_amd.compiler import layout as L
 from enceladus_amd.language import core
@@ -194,3 +196,38 @@ def test_two_privatised_histograms_get_their_own_bins():
                                                       BLOCK=1024)).source
     assert "ek_bins0[256]" in src and "ek_bins1[128]" in src
     assert src.count("__HIP_MEMORY_SCOPE_AGENT") == 2      # one flush per histogram
+
+
+@enceladus.jit
+def _split_kinds(x_ptr, out_ptr, M: tl.constexpr, CASE: tl.constexpr):
+    rm = tl.arange(0, M)
+    if CASE == "register":
+        v = tl.load(x_ptr + rm[:, None] * 2 + tl.arange(0, 2)[None, :])
+    else:
+        v = tl.load(x_ptr + tl.arange(0, 2)[:, None] * M + rm[None, :]).T
+    a, b = tl.split(v)
+    tl.store(out_ptr + rm, a - b)
+
+
+def test_split_of_register_or_lane_bit_needs_no_lds():
+    """The split coordinate in a register selects registers; in a lane it becomes a pair
+    of shuffles. Neither goes through LDS (reference: codegen/msl.py:693-747 keeps the
+    same two cases free)."""
+    x = np.zeros(4, np.float32)
+    reg = codegen_hip.generate(_split_kinds.ir_for(x, x, M=256, CASE="register"))
+    lane = codegen_hip.generate(_split_kinds.ir_for(x, x, M=64, CASE="lane", num_warps=1))
+    assert reg.lds_bytes == 0 and "ek::shfl(" not in reg.source
+    assert lane.lds_bytes == 0 and "ek::shfl(" in lane.source
+
+
+def test_reshape_is_a_view():
+    """A reshape of a loaded tile relabels layout bits: no LDS round trip."""
+    x = np.zeros(4, np.float32)
+    f = _split_kinds.ir_for(x, x, M=256, CASE="register")
+    assert any(op.name == "split" for op in ir.walk(f.body))
+    lay = L.Layout((8, 16), ((1, 0), (1, 1)), ((1, 2), (1, 3), (0, 0), (0, 1), (0, 2), None),
+                 (None,))
+    flat = lay.reshape((128,))
+    assert flat.reg == ((0, 0), (0, 1)) and flat.lane[:5] == ((0, 2), (0, 3), (0, 4),
+                                                               (0, 5), (0, 6))
+    assert flat.reshape((8, 16)).key() == lay.key()

@@ -93,3 +93,59 @@ def test_calling_kernel_directly_raises():
 def test_tl_names_outside_kernels_raise():
     with pytest.raises(RuntimeError):
         tl.program_id(0)
+
+
+# -- join / split / reduce / associative_scan -----------------------------------------
+
+@enceladus.jit
+def _join_kernel(x_ptr, y_ptr, CASE: tl.constexpr):
+    r = tl.arange(0, 16)
+    x = tl.load(x_ptr + r)
+    if CASE == "dtype":
+        tl.join(x, tl.load(y_ptr + r))
+    elif CASE == "literal":
+        tl.store(x_ptr + tl.arange(0, 32), tl.reshape(tl.join(x, 3), (32,)))
+    elif CASE == "split_shape":
+        tl.split(x)
+    elif CASE == "pointer":
+        tl.join(x_ptr + r, x_ptr + r)
+    elif CASE == "plain_combine":
+        tl.reduce(x, 0, _plain_add)
+    elif CASE == "arity":
+        tl.reduce((x, x), 0, _one_of_two)
+    elif CASE == "scan_axis":
+        tl.associative_scan(x, None, _one_of_two)
+
+
+def _plain_add(a, b):
+    return a + b
+
+
+@enceladus.jit
+def _one_of_two(a0, a1, b0, b1):
+    return a0 + b0
+
+
+def _jk(case, ydt=np.float32):
+    return _join_kernel.ir_for(np.zeros(4, np.float32), np.zeros(4, ydt), CASE=case)
+
+
+def test_join_split_errors():
+    with pytest.raises(CompilationError, match="one dtype"):
+        _jk("dtype", np.float16)
+    f = _jk("literal")
+    j = [op for op in ir.walk(f.body) if op.name == "join"][0]
+    assert j.result.type == ir.TType((16, 2), tl.float32)
+    with pytest.raises(CompilationError, match="last dimension is 2"):
+        _jk("split_shape")
+    with pytest.raises(CompilationError, match="pointers"):
+        _jk("pointer")
+
+
+def test_combine_function_errors():
+    with pytest.raises(CompilationError, match="@enceladus.jit"):
+        _jk("plain_combine")
+    with pytest.raises(CompilationError, match="returns 1 values for 2 inputs"):
+        _jk("arity")
+    with pytest.raises(CompilationError, match="needs an `axis`"):
+        _jk("scan_axis")
