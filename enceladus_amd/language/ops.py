@@ -1,10 +1,10 @@
 """The `tl` builtins: each one builds IR when a kernel is compiled.
 
 Calling a builtin outside a kernel raises. Signatures and semantics follow the reference
-language (reference: src/enceladus/language/ops.py, lines 136-2074: program_id :141, arange :179, full :203, load :305, store :365,
-make_tensor_descriptor :437, where :557, to :668, sum :983, max :1015, dot :1244,
-atomic_add :1943, cumsum :2064, join :840, split :875, reduce :1100,
-associative_scan :2097).
+language (reference: src/enceladus/language/ops.py, lines 136-2074: program_id :141,
+arange :179, full :203, load :305, store :365, make_tensor_descriptor :437, where :557,
+to :668, join :840, split :875, sum :983, max :1015, reduce :1100, dot :1244,
+atomic_add :1943, cumsum :2064, associative_scan :2097).
 """
 
 from __future__ import annotations
