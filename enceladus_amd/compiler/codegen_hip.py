@@ -165,7 +165,8 @@ class Emitter:
         self.inplace: set[int] = set()
         self.extra_smem: list[tuple[str, int]] = []
         self.asserts: list[dict] = []
-        self.split_bit: dict[int, int] = {}
+        self.split_bit: dict[int, tuple] = {}
+        self.int_dots: set[int] = set()
 
     # ------------------------------------------------------------------ utilities
     def fresh(self, hint="v") -> str:
@@ -268,20 +269,28 @@ class Emitter:
         k order when one dot's result feeds another dot's A operand (attention's P), so
         the product's registers are the next MFMA's operand registers."""
         dw = self.opt.get("dot_warps")
-        dots = [op for op in ir.walk(fn.body) if op.name == "dot"]
+        dots = []
         base = {}
-        for d in dots:
+        for d in (op for op in ir.walk(fn.body) if op.name == "dot"):
             a, b = d.operands[0], d.operands[1]
+            adt = a.type.dtype
+            if adt.is_int() and (adt is not core.int8 or self.opt.get("no_int8_mfma")):
+                self.int_dots.add(d.result.id)   # multiply-adds from LDS
+                continue
             try:
                 base[d] = LY.plan_dot(a.type.shape[0], b.type.shape[1], a.type.shape[1],
-                                      self.nw, a.type.dtype.name, dw)
+                                      self.nw, adt.name, dw)
             except ValueError as e:
+                if adt.is_int():
+                    self.int_dots.add(d.result.id)
+                    continue
                 raise CompilationError(str(e)) from None
+            dots.append(d)
         trans, korder = set(), {}
         if not self.opt.get("no_dot_transpose"):
             for d2 in dots:
                 d1 = self._dot_source(d2.operands[0])
-                if d1 is None or d1 is d2:
+                if d1 is None or d1 is d2 or d1 not in base:
                     continue
                 p1, p2 = base[d1], base[d2]
                 if p1.inst.m != 32 or p2.inst.m != 32 or p2.inst.k != 16:
@@ -312,7 +321,7 @@ class Emitter:
             u = self.uses[v2.id][0]
         else:
             v2 = v
-        if u.name != "dot":
+        if u.name != "dot" or u.result.id not in self.dot_plans:
             return None
         plan = self.dot_plans[u.result.id]
         if u.operands[0].id == v2.id:
@@ -449,9 +458,11 @@ class Emitter:
                                  max(1, 16 // es), self.nw)
             self.lay[res.id] = lay
         elif n == "dot":
-            plan = self.dot_plans[op.result.id]
             self.kind[res.id] = "anchored"
-            self.lay[res.id] = LY.mfma_acc(plan)
+            if res.id in self.int_dots:
+                self.lay[res.id] = self.default_layout(res)
+            else:
+                self.lay[res.id] = LY.mfma_acc(self.dot_plans[res.id])
         elif n == "reduce":
             src = op.operands[0]
             sl = self.lay[src.id] if self._anch(src) else self.default_layout(src)
@@ -1925,9 +1936,52 @@ class Emitter:
         self.emit(f"    for (int j = 0; j < {n}; j += {V}) ek::vload<{T}, {V}>(&{dst}[j], "
                   f"&{sm}[{idx}]);")
 
+    def op_dot_int(self, op):
+        """Integer product without MFMA (uint8, 16- and 32-bit operands, or tiles the i8
+        MFMAs can't take): both operands go to LDS as int32 (A rows padded by one word so
+        a wave's different rows hit different banks), then every thread accumulates its
+        own outputs over k. Arithmetic is unsigned 32-bit, so products and sums wrap
+        modulo 2^32 as the integer tl.dot defines."""
+        a, b, c = op.operands
+        res = op.result
+        lay = self.lay[res.id]
+        M, K = a.type.shape
+        N = b.type.shape[1]
+        pa = K + 1
+        self.need_lds((M * pa + K * N) * 4)
+        la = self.lay[a.id] if self.kind.get(a.id) == "anchored" else self.default_layout(a)
+        lb = self.lay[b.id] if self.kind.get(b.id) == "anchored" else self.default_layout(b)
+        xa, xb = self.array(a, la), self.array(b, lb)
+        nm = self.fresh("acc")
+        self.emit(f"int32_t {nm}[{lay.nregs}];")
+        self.emit("#pragma unroll")
+        self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = "
+                  f"(int32_t)({self.elem(c, lay, 'r')});")
+        mr, nr = self.coord(lay, 0, "r"), self.coord(lay, 1, "r")
+        self.emit("{")
+        self.emit("  int32_t* sa = reinterpret_cast<int32_t*>(ek_smem);")
+        self.emit(f"  int32_t* sb = sa + {M * pa};")
+        self.emit("  __syncthreads();")
+        self.emit("  #pragma unroll")
+        self.emit(f"  for (int r = 0; r < {la.nregs}; ++r) sa[({self.coord(la, 0, 'r')}) * "
+                  f"{pa} + ({self.coord(la, 1, 'r')})] = (int32_t){xa}[r];")
+        self.emit("  #pragma unroll")
+        self.emit(f"  for (int r = 0; r < {lb.nregs}; ++r) sb[({self.coord(lb, 0, 'r')}) * "
+                  f"{N} + ({self.coord(lb, 1, 'r')})] = (int32_t){xb}[r];")
+        self.emit("  __syncthreads();")
+        self.emit(f"  for (int k = 0; k < {K}; ++k) {{")
+        self.emit("    #pragma unroll")
+        self.emit(f"    for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = (int32_t)((uint32_t){nm}[r]"
+                  f" + (uint32_t)sa[({mr}) * {pa} + k] * (uint32_t)sb[k * {N} + ({nr})]);")
+        self.emit("  }")
+        self.emit("}")
+        self.define(res, nm)
+
     def op_dot(self, op):
         a, b, c = op.operands
         res = op.result
+        if res.id in self.int_dots:
+            return self.op_dot_int(op)
         plan = self.dot_plans[res.id]
         la, lb = LY.mfma_operand(plan, "a"), LY.mfma_operand(plan, "b")
         lc = self.lay[res.id]
@@ -1939,9 +1993,15 @@ class Emitter:
         cdt = res.type.dtype
         nacc = 16 if ins.m == 32 else 4
         single = len(self.uses.get(c.id, [])) == 1
-        if cdt is core.float32 and self.kind.get(c.id) == "anchored" and single and \
-                self.lay[c.id].key() == lc.key():
+        if cdt in (core.float32, core.int32) and self.kind.get(c.id) == "anchored" and \
+                single and self.lay[c.id].key() == lc.key():
             nm = self.name[c.id]
+        elif cdt is core.int32:
+            nm = self.fresh("acc")
+            e = self.elem(c, lc, "r")
+            self.emit(f"int32_t {nm}[{lc.nregs}];")
+            self.emit("#pragma unroll")
+            self.emit(f"for (int r = 0; r < {lc.nregs}; ++r) {nm}[r] = {e};")
         else:
             nm = self.fresh("acc")
             e = self.elem(c, lc, "r")
@@ -1981,7 +2041,7 @@ class Emitter:
         self.emit(f"    for (int in_ = 0; in_ < {tn}; ++in_) "
                   f"ek::{ins.fn}(&{nm}[(im * {tn} + in_) * {nacc}], {x}, {y});")
         self.emit("}")
-        if cdt is not core.float32:
+        if cdt not in (core.float32, core.int32):
             out = self.fresh("acch")
             self.emit(f"{ctype(cdt)} {out}[{lc.nregs}];")
             self.emit(f"for (int r = 0; r < {lc.nregs}; ++r) {out}[r] = ek::rnd<{ctype(cdt)}>"

@@ -297,6 +297,14 @@ class MfmaShape:
 
 def pick_mfma(pm: int, pn: int, bk: int, dtype_name: str) -> MfmaShape:
     """Chooses the gfx950 MFMA for a per-warp tile pm x pn and depth bk."""
+    if dtype_name == "i8":
+        if pm % 32 == 0 and pn % 32 == 0 and bk % 16 == 0:
+            if bk % 32 == 0:
+                return MfmaShape(32, 32, 32, 16, "mfma_32x32x32")
+            return MfmaShape(32, 32, 16, 8, "mfma_32x32x16")
+        if bk % 64 == 0:
+            return MfmaShape(16, 16, 64, 16, "mfma_16x16x64")
+        return MfmaShape(16, 16, 32, 8, "mfma_16x16x32")
     if dtype_name == "fp32":
         if pm % 32 == 0 and pn % 32 == 0 and bk % 2 == 0:
             return MfmaShape(32, 32, 2, 1, "mfma_32x32x2")

@@ -294,7 +294,11 @@ template <typename V, typename T> EK_INLINE V pack(const T* p) {
   __builtin_memcpy(&v, p, sizeof(V));
   return v;
 }
-template <typename V> EK_INLINE void unpack(float* p, V v) { __builtin_memcpy(p, &v, sizeof(V)); }
+template <typename V, typename T> EK_INLINE void unpack(T* p, V v) {
+  __builtin_memcpy(p, &v, sizeof(V));
+}
+typedef int i32x16m __attribute__((ext_vector_type(16)));
+typedef int i32x4m __attribute__((ext_vector_type(4)));
 
 // D[32x32] += A[32x16] * B[16x32], fp16/bf16 inputs, 8 elements per lane.
 EK_INLINE void mfma_32x32x16(float* acc, const _Float16* a, const _Float16* b) {
@@ -350,6 +354,31 @@ EK_INLINE void mfma_16x16x4(float* acc, const float* a, const float* b) {
 EK_INLINE void mfma_32x32x2(float* acc, const float* a, const float* b) {
   f32x16 c = pack<f32x16>(acc);
   c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[0], b[0], c, 0, 0, 0);
+  unpack(acc, c);
+}
+// int8 inputs, int32 accumulator; integer sums wrap modulo 2^32.
+// D[32x32] += A[32x32] * B[32x32], 16 elements per lane (gfx950).
+EK_INLINE void mfma_32x32x32(int32_t* acc, const int8_t* a, const int8_t* b) {
+  i32x16m c = pack<i32x16m>(acc);
+  c = __builtin_amdgcn_mfma_i32_32x32x32_i8(pack<i32x4m>(a), pack<i32x4m>(b), c, 0, 0, 0);
+  unpack(acc, c);
+}
+// D[16x16] += A[16x64] * B[64x16], 16 elements per lane (gfx950).
+EK_INLINE void mfma_16x16x64(int32_t* acc, const int8_t* a, const int8_t* b) {
+  i32x4m c = pack<i32x4m>(acc);
+  c = __builtin_amdgcn_mfma_i32_16x16x64_i8(pack<i32x4m>(a), pack<i32x4m>(b), c, 0, 0, 0);
+  unpack(acc, c);
+}
+// D[32x32] += A[32x16] * B[16x32], 8 elements per lane.
+EK_INLINE void mfma_32x32x16(int32_t* acc, const int8_t* a, const int8_t* b) {
+  i32x16m c = pack<i32x16m>(acc);
+  c = __builtin_amdgcn_mfma_i32_32x32x16_i8(pack<long>(a), pack<long>(b), c, 0, 0, 0);
+  unpack(acc, c);
+}
+// D[16x16] += A[16x32] * B[32x16], 8 elements per lane.
+EK_INLINE void mfma_16x16x32(int32_t* acc, const int8_t* a, const int8_t* b) {
+  i32x4m c = pack<i32x4m>(acc);
+  c = __builtin_amdgcn_mfma_i32_16x16x32_i8(pack<long>(a), pack<long>(b), c, 0, 0, 0);
   unpack(acc, c);
 }
 

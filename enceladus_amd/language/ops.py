@@ -730,7 +730,12 @@ _DOT_FLOAT = (core.float16, core.bfloat16, core.float32)
 @builtin()
 def dot(ctx, input, other, acc=None, input_precision=None, allow_tf32=None,
         max_num_imprecise_acc=None, out_dtype=None):
-    """Matrix product of two 2D tiles, accumulated in fp32 (floats) or int32 (ints)."""
+    """Matrix product of two 2D tiles, accumulated in fp32 (floats) or int32 (ints).
+
+    int8 operands run on the i8 MFMAs (v_mfma_i32_32x32x32_i8 and relatives); uint8,
+    16- and 32-bit integer operands run as 32-bit multiply-adds from LDS. Integer
+    products and sums wrap modulo 2^32, as in the reference (language/ops.py:1244-1270).
+    """
     b = ctx.b
     a = _tile(ctx, input, "dot")
     bt = _tile(ctx, other, "dot")
@@ -759,9 +764,14 @@ def dot(ctx, input, other, acc=None, input_precision=None, allow_tf32=None,
             raise CompilationError(f"the tl.dot accumulator must be {m}x{n}, got "
                                    f"{accv.type.shape}")
     if adt.is_int():
+        if adt.primitive_bitwidth not in (8, 16, 32) or adt.is_bool():
+            raise CompilationError(f"tl.dot takes 8-, 16- or 32-bit integer operands, got {adt}")
         if out_dt is not core.int32:
             raise CompilationError("tl.dot accumulates integer operands in int32")
-        raise CompilationError("integer tl.dot isn't supported by the MI355X backend yet")
+        if a.type.shape[1] % 8:
+            raise CompilationError(f"tl.dot needs a K dimension that is a multiple of 8, got "
+                                   f"{a.type.shape[1]}")
+        return b.create("dot", [a, bt, accv], [ir.TType((m, n), out_dt)]).result
     if adt not in _DOT_FLOAT:
         raise CompilationError(f"tl.dot supports float16, bfloat16 and float32 operands, "
                                f"got {adt}")

@@ -231,3 +231,23 @@ def test_reshape_is_a_view():
     assert flat.reg == ((0, 0), (0, 1)) and flat.lane[:5] == ((0, 2), (0, 3), (0, 4),
                                                                (0, 5), (0, 6))
     assert flat.reshape((8, 16)).key() == lay.key()
+
+
+def test_integer_dot_lowering():
+    """int8 products run on the i8 MFMAs; uint8/16/32-bit ones as LDS multiply-adds; 64-bit
+    operands are rejected (reference: language/ops.py:1244-1270)."""
+    from tests.test_gpu_int_dot import _int_matmul
+    c = np.zeros(4, np.int32)
+
+    def src(dt, bm, bn, bk, nw=4):
+        z = np.zeros(4, dt)
+        return codegen_hip.generate(_int_matmul.ir_for(z, z, c, 64, BM=bm, BN=bn, BK=bk,
+                                                       ACC=False, num_warps=nw)).source
+    assert "ek::mfma_32x32x32(" in src(np.int8, 64, 64, 64)
+    assert "ek::mfma_16x16x64(" in src(np.int8, 16, 16, 64, 1)
+    for dt in (np.uint8, np.int16, np.int32):
+        s = src(dt, 32, 32, 16)
+        assert "mfma" not in s and "(uint32_t)sa[" in s
+    from enceladus_amd.compiler.errors import CompilationError
+    with pytest.raises(CompilationError, match="8-, 16- or 32-bit"):
+        src(np.int64, 32, 32, 16)
