@@ -1353,6 +1353,19 @@ class Emitter:
             return (str(st), str(st + v.type.shape[0] - 1))
         if n in ("splat", "broadcast", "expand_dims", "hint"):
             return self.interval(op.operands[0], depth + 1)
+        if n == "cast":
+            # a widening integer cast (64-bit index math) keeps the bounds; the bound
+            # expressions are evaluated in the wider type
+            x = op.operands[0]
+            if x.type.ptr or not x.type.dtype.is_int() or x.type.dtype.is_bool() or \
+                    x.type.dtype.primitive_bitwidth > v.type.dtype.primitive_bitwidth or \
+                    (x.type.dtype.kind == "uint") != (v.type.dtype.kind == "uint"):
+                return None
+            a = self.interval(x, depth + 1)
+            if a is None:
+                return None
+            t = ctype(v.type.dtype)
+            return (f"(({t})({a[0]}))", f"(({t})({a[1]}))")
         if n == "binary" and op.attrs["op"] in ("add", "sub", "mul"):
             a = self.interval(op.operands[0], depth + 1)
             b = self.interval(op.operands[1], depth + 1)
@@ -2352,7 +2365,7 @@ class Emitter:
     def _stage_buffer_ok(self, info, d, W: int) -> bool:
         """Whether a stage can load through raw buffer loads: 32-bit byte offsets, aligned
         rows, and column chunks of W elements that lie wholly inside or outside the tile."""
-        if self.opt.get("no_buffer_loads") or d["base_v"].facts.get("idx64"):
+        if self.opt.get("no_buffer_loads") or d["base_v"].facts.get("span2g"):
             return False
         div = lambda v: self.axis.get(v).div[0]  # noqa: E731
         if div(d["base_v"]) < 2 * W or div(d["stride_v"][0]) % W:
@@ -2605,7 +2618,7 @@ class Emitter:
         # Buffer loads (hardware bounds checks) send a 16-byte chunk that is not wholly inside
         # its row out of range, so they need K and N known to be multiples of 8; and no
         # operand may span >= 2 GiB (32-bit byte offsets).
-        big = any(v.facts.get("idx64") for v in (A["base_v"], B["base_v"]))
+        big = any(v.facts.get("span2g") for v in (A["base_v"], B["base_v"]))
         whole = all(self.axis.get(v).div[0] % 8 == 0 for v in (A["shape_v"][1], B["shape_v"][1]))
         buf = not (big or not whole or self.opt.get("no_buffer_loads"))
         bm, bn, bk = g["bm"], g["bn"], g["bk"]

@@ -25,7 +25,7 @@ import sys
 import threading
 from pathlib import Path
 
-from enceladus_amd.compiler import codegen_hip, frontend, ir
+from enceladus_amd.compiler import codegen_hip, frontend, ir, widen
 from enceladus_amd.runtime import hip
 
 log = logging.getLogger("enceladus")
@@ -192,4 +192,7 @@ def compile_ir(fn: ir.Func, options: dict | None = None) -> CompiledKernel:
 
 
 def build_module(jfn, arg_types, arg_facts, constexprs, num_warps, options) -> ir.Func:
-    return frontend.build_ir(jfn.fn, arg_types, arg_facts, constexprs, num_warps, options)
+    fn = frontend.build_ir(jfn.fn, arg_types, arg_facts, constexprs, num_warps, options)
+    if widen.needs_idx64(fn):
+        widen.widen_index_math(fn)
+    return fn

@@ -91,19 +91,37 @@ def arg_facts(value: Any) -> dict:
             facts["divisibility"] = 16   # copied into a fresh 16-byte-aligned allocation
         elif p is not None and p % 16 == 0:
             facts["divisibility"] = 16
-        if _span_bytes(value) >= (1 << 31) - 64:
-            facts["idx64"] = True        # offsets may not fit 32-bit byte offsets
+        last = _last_index(value)
+        if (last + 1) * T.elem_dtype(value).itemsize >= (1 << 31) - 64:
+            facts["span2g"] = True       # byte offsets may not fit 32 bits: no buffer loads
+        if last > MAX_ELEMENT_INDEX:
+            facts["idx64"] = True        # element offsets need 64-bit index math
         return facts
     return {}
 
 
-def _span_bytes(value) -> int:
-    shape = tuple(getattr(value, "shape", ()))
+# The largest element offset from an array argument's first element that 32-bit index
+# math reaches; launches with a larger span compile an `idx64` variant with 64-bit index
+# math (reference: runtime/launcher.py:42-48).
+MAX_ELEMENT_INDEX = (1 << 31) - 1
+# facts that stay in the specialization even for do_not_specialize parameters
+REQUIRED_FACTS = ("idx64", "span2g")
+
+
+def _last_index(value) -> int:
+    """How many elements past the first the last element of array `value` lies (NumPy
+    arrays are copied to a contiguous allocation; others use their strides)."""
+    shape = tuple(int(d) for d in getattr(value, "shape", ()))
+    if 0 in shape:
+        return -1
+    stride = getattr(value, "stride", None)
+    if callable(stride) and not isinstance(value, np.ndarray):
+        st = tuple(int(x) for x in stride())
+        return sum((n - 1) * abs(x) for n, x in zip(shape, st))
     n = 1
     for d in shape:
-        n *= int(d)
-    es = T.elem_dtype(value).itemsize
-    return n * es
+        n *= d
+    return n - 1
 
 
 @dataclass(frozen=True)
@@ -247,7 +265,7 @@ class JITFunction:
             types[p.name] = arg_type(v)
             f = arg_facts(v)
             if p.do_not_specialize:
-                f = {}
+                f = {k: x for k, x in f.items() if k in REQUIRED_FACTS}
             facts[p.name] = f
         return types, facts, consts
 

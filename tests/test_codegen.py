@@ -251,3 +251,51 @@ def test_integer_dot_lowering():
     from enceladus_amd.compiler.errors import CompilationError
     with pytest.raises(CompilationError, match="8-, 16- or 32-bit"):
         src(np.int64, 32, 32, 16)
+
+
+@enceladus.jit
+def _offsets_kernel(x_ptr, out_ptr, n, BLOCK: tl.constexpr):
+    pid = tl.program_id(0)
+    offs = pid * BLOCK + tl.arange(0, BLOCK)
+    mask = offs < n
+    v = tl.load(x_ptr + offs, mask=mask)
+    tl.store(out_ptr + offs, v + offs.to(tl.uint8), mask=mask)
+
+
+def test_idx64_widens_pointer_offsets_and_masks():
+    """An argument spanning more than 2^31 elements gets 64-bit index math: every
+    pointer offset and the mask reading it are int64, a use as data keeps int32
+    (reference: compiler/passes/widen_index.py)."""
+    from enceladus_amd.compiler import frontend, widen
+    t = ir.TType((), core.uint8, ptr=True)
+    types = {"x_ptr": t, "out_ptr": t, "n": ir.TType((), core.int64)}
+    facts = {"x_ptr": {"idx64": True}, "out_ptr": {"idx64": True}, "n": {}}
+    fn = frontend.build_ir(_offsets_kernel.fn, types, facts, {"BLOCK": 1024})
+    assert widen.widen_index_math(fn) >= 3
+    ops = list(ir.walk(fn.body))
+    adds = [op for op in ops if op.name == "ptr_add"]
+    assert adds and all(op.operands[1].type.dtype is core.int64 for op in adds)
+    cmps = [op for op in ops if op.name == "binary" and op.attrs["op"] == "lt"]
+    assert cmps and all(o.type.dtype is core.int64 for op in cmps for o in op.operands)
+    casts = [op for op in ops if op.name == "cast" and op.result.type.dtype is core.uint8]
+    assert casts and casts[0].operands[0].type.dtype is core.int32
+    src = codegen_hip.generate(fn).source
+    assert "(int64_t)" in src
+    # without the fact nothing changes
+    fn32 = frontend.build_ir(_offsets_kernel.fn, types, {"x_ptr": {}, "out_ptr": {}, "n": {}},
+                             {"BLOCK": 1024})
+    assert not widen.needs_idx64(fn32)
+
+
+def test_idx64_fact_from_element_span():
+    """`idx64` follows the element span from strides (no memory needed to test it)."""
+    from enceladus_amd.runtime import jit
+    import torch
+    assert "idx64" not in jit.arg_facts(torch.empty(16, dtype=torch.uint8))
+
+    class _Strided:
+        shape = (2, 1 << 30)
+
+        def stride(self):
+            return (1 << 31, 1)
+    assert jit._last_index(_Strided()) == (1 << 31) + (1 << 30) - 1 > jit.MAX_ELEMENT_INDEX
