@@ -12,12 +12,13 @@ from enceladus_amd.compiler.errors import (  # noqa: F401
     CompilationError, DeviceAssertionError, HipError,
 )
 from enceladus_amd.language.core import constexpr  # noqa: F401
+from enceladus_amd.runtime.debug import capture, lazy_mlx  # noqa: F401
 from enceladus_amd.runtime.device import Capabilities, get_device, synchronize  # noqa: F401
 from enceladus_amd.runtime.jit import JITFunction, cdiv, jit, next_power_of_2  # noqa: F401
 from enceladus_amd.runtime.raw import hip_kernel, metal_kernel  # noqa: F401
 from enceladus_amd.runtime.tensor import (  # noqa: F401
-    Tensor, element_dtype, element_strides, empty, from_numpy, new_empty, new_zeros, randn,
-    zeros,
+    Tensor, arange, async_numpy, element_dtype, element_strides, empty, empty_like, from_numpy,
+    full, new_empty, new_zeros, ones, rand, randn, zeros, zeros_like,
 )
 
 MetalError = HipError  # the reference's runtime error name, kept for drop-in code

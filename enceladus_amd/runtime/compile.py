@@ -152,8 +152,13 @@ class CompiledKernel:
             kernarg = kernarg[:self.packed_size] + extra
             kernarg += b"\0" * ((-len(kernarg)) % 8)
         buf = ctypes.create_string_buffer(kernarg, len(kernarg))
+        from enceladus_amd.runtime import debug
+        t0 = debug.before_launch(stream) if debug._active is not None else None
         hip.call("ek_launch", ctypes.c_void_p(stream or None), self.function(), gx, gy, gz,
                  self.gen.block, 1, 1, 0, buf, len(kernarg))
+        if t0 is not None:
+            debug.after_launch(t0, stream, self.name, (gx, gy, gz), self.gen.block,
+                               self.gen.lds_bytes)
 
 
 _CAP = None

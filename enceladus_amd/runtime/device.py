@@ -51,7 +51,11 @@ def has_gpu() -> bool:
 
 
 def synchronize() -> None:
+    """Waits for all GPU work, then copies back host arrays that asynchronous launches
+    wrote (`enceladus.async_numpy`)."""
     hip.call("ek_device_sync")
+    from enceladus_amd.runtime import tensor
+    tensor.flush_pending()
 
 
 def current_stream() -> int:

@@ -114,8 +114,10 @@ def _last_index(value) -> int:
     shape = tuple(int(d) for d in getattr(value, "shape", ()))
     if 0 in shape:
         return -1
+    if isinstance(value, np.ndarray):
+        return sum((n - 1) * abs(x) // value.itemsize for n, x in zip(shape, value.strides))
     stride = getattr(value, "stride", None)
-    if callable(stride) and not isinstance(value, np.ndarray):
+    if callable(stride):
         st = tuple(int(x) for x in stride())
         return sum((n - 1) * abs(x) for n, x in zip(shape, st))
     n = 1
@@ -192,17 +194,19 @@ class Launcher:
             hip.call("ek_memset", ctypes.c_void_p(self._abuf.ptr), 0, 20, None)
             packed.append(self._abuf.ptr)
         self.ck.launch_raw(grid, self.ck.pack(packed), stream)
-        if any(b.host is not None for b in bindings) or asserts:
+        if not asserts:
+            T.complete_bindings(bindings)
+        else:
             from enceladus_amd.runtime import hip
+            T.flush_pending()
             hip.call("ek_device_sync")
             for b in bindings:
                 T.finish_binding(b)
-            if asserts:
-                rec = self._abuf.numpy()
-                if rec[0]:
-                    a = asserts[int(rec[1])]
-                    raise DeviceAssertionError(a["msg"], a["loc"],
-                                               (int(rec[2]), int(rec[3]), int(rec[4])))
+            rec = self._abuf.numpy()
+            if rec[0]:
+                a = asserts[int(rec[1])]
+                raise DeviceAssertionError(a["msg"], a["loc"],
+                                           (int(rec[2]), int(rec[3]), int(rec[4])))
 
 
 class JITFunction:

@@ -174,12 +174,13 @@ class HipKernel:
         kern = pack(self.params, vals)
         buf = ctypes.create_string_buffer(kern, len(kern))
         stream = D.current_stream()
+        from enceladus_amd.runtime import debug
+        t0 = debug.before_launch(stream) if debug._active is not None else None
         hip.call("ek_launch", ctypes.c_void_p(stream or None), self.function(), grid[0],
                  grid[1], grid[2], tg[0], tg[1], tg[2], 0, buf, len(kern))
-        if any(b.host is not None for b in bindings):
-            hip.call("ek_device_sync")
-            for b in bindings:
-                T.finish_binding(b)
+        if t0 is not None:
+            debug.after_launch(t0, stream, self.name, grid, tg[0] * tg[1] * tg[2], 0)
+        T.complete_bindings(bindings)
 
 
 def hip_kernel(source: str, name: str, options=()) -> HipKernel:

@@ -97,10 +97,50 @@ class Tensor:
                              versioned=versioned)
 
 
+def _shape_arg(shape) -> tuple:
+    if len(shape) == 1 and not isinstance(shape[0], (int, np.integer)):
+        shape = tuple(shape[0])
+    return tuple(int(s) for s in shape)
+
+
 def empty(shape, dtype=core.float32) -> Tensor:
     if isinstance(shape, int):
         shape = (shape,)
     return Tensor(shape, _as_dtype(dtype))
+
+
+def full(shape, value, dtype=core.float32) -> Tensor:
+    """A tensor filled with `value` (reference: runtime/tensor.py:290-302)."""
+    if isinstance(shape, int):
+        shape = (shape,)
+    dt = _as_dtype(dtype)
+    return from_numpy(np.full(tuple(shape), value, dt.to_numpy()), dt)
+
+
+def ones(shape, dtype=core.float32) -> Tensor:
+    return full(shape, 1, dtype)
+
+
+def rand(*shape, dtype=core.float32, seed: int | None = None) -> Tensor:
+    """Samples from the uniform distribution on [0, 1) (reference: tensor.py:316-321)."""
+    shape = _shape_arg(shape)
+    v = np.random.default_rng(seed).random(shape, dtype=np.float32)
+    return from_numpy(v.astype(_as_dtype(dtype).to_numpy()), dtype)
+
+
+def arange(start: int, end: int | None = None, step: int = 1, dtype=core.int32) -> Tensor:
+    if end is None:
+        start, end = 0, start
+    dt = _as_dtype(dtype)
+    return from_numpy(np.arange(start, end, step).astype(dt.to_numpy()), dt)
+
+
+def empty_like(t: Any, dtype=None) -> Tensor:
+    return empty(tuple(t.shape), dtype if dtype is not None else elem_dtype(t))
+
+
+def zeros_like(t: Any, dtype=None) -> Tensor:
+    return zeros(tuple(t.shape), dtype if dtype is not None else elem_dtype(t))
 
 
 def zeros(shape, dtype=core.float32) -> Tensor:
@@ -117,9 +157,10 @@ def from_numpy(a: np.ndarray, dtype=None) -> Tensor:
     return t.copy_from_numpy(a)
 
 
-def randn(*shape, dtype=core.float32, seed: int = 0) -> Tensor:
+def randn(*shape, dtype=core.float32, seed: int | None = None) -> Tensor:
+    """Samples from the standard normal distribution (reference: tensor.py:308-313)."""
     rng = np.random.default_rng(seed)
-    return from_numpy(rng.standard_normal(shape, dtype=np.float32).astype(
+    return from_numpy(rng.standard_normal(_shape_arg(shape), dtype=np.float32).astype(
         _as_dtype(dtype).to_numpy()), dtype)
 
 
@@ -208,14 +249,78 @@ def is_array_like(x: Any) -> bool:
 class Binding:
     """One array argument bound for a launch: its device pointer, plus a copy-back."""
 
-    __slots__ = ("ptr", "host", "dev", "writeback", "keep")
+    __slots__ = ("ptr", "host", "dev", "writeback", "keep", "key")
 
-    def __init__(self, ptr, host=None, dev=None, keep=None):
+    def __init__(self, ptr, host=None, dev=None, keep=None, key=None):
         self.ptr = ptr
         self.host = host
         self.dev = dev
         self.writeback = False
         self.keep = keep
+        self.key = key
+
+
+# -- asynchronous host arrays (reference: runtime/interop.py:495-503) --------------------
+# By default a launch that takes a NumPy (or CPU torch) array copies it to HBM, waits for
+# the kernel and copies it back. With `async_numpy(True)` the launch returns at once; the
+# device copy stays live and later launches on the same array use it (so chained kernels
+# see each other's writes), and `enceladus.synchronize()` copies every written array back.
+_async = False
+_pending: dict[tuple[int, int], Binding] = {}
+
+
+def async_numpy(enabled: bool = True) -> None:
+    """Sets whether launches that touch host arrays return before the GPU finishes.
+    With it on, call `enceladus.synchronize()` before reading or writing those arrays on
+    the host. Turning it off synchronizes first."""
+    global _async
+    if not enabled and _async:
+        flush_pending()
+    _async = bool(enabled)
+
+
+def flush_pending() -> None:
+    """Waits for the device and copies back every host array a pending launch wrote."""
+    if not _pending:
+        return
+    hip.call("ek_device_sync")
+    items = list(_pending.values())
+    _pending.clear()
+    for b in items:
+        finish_binding(b)
+
+
+def complete_bindings(bindings: list) -> None:
+    """After a launch: copy written host arrays back now, or leave them pending."""
+    hosts = [b for b in bindings if b.host is not None]
+    if not hosts:
+        return
+    if _async:
+        for b in hosts:
+            p = _pending.get(b.key)
+            if p is None:
+                _pending[b.key] = b
+            else:
+                p.writeback = p.writeback or b.writeback
+        return
+    hip.call("ek_device_sync")
+    for b in hosts:
+        finish_binding(b)
+
+
+def _bind_host(a: np.ndarray, n: int) -> Binding:
+    start = a.__array_interface__["data"][0] if a.size else 0
+    key = (start, n)
+    if _pending:
+        p = _pending.get(key)
+        if p is not None:
+            return Binding(p.dev.ptr, host=a, dev=p.dev, key=key)
+        if any(s < start + n and start < s + m for s, m in _pending):
+            flush_pending()       # another view of pending memory: settle it first
+    dev = Tensor((max(n, 1),), core.uint8)
+    if n:
+        hip.call("ek_memcpy_h2d", ctypes.c_void_p(dev.ptr), ctypes.c_void_p(start), n, None)
+    return Binding(dev.ptr, host=a, dev=dev, key=key)
 
 
 def bind_array(x: Any) -> Binding:
@@ -225,22 +330,9 @@ def bind_array(x: Any) -> Binding:
         if x.device.type == "cuda":
             return Binding(int(x.data_ptr()), keep=x)
         a = x.detach().numpy()
-        dev = Tensor((a.nbytes,), core.uint8)
-        if a.nbytes:
-            hip.call("ek_memcpy_h2d", ctypes.c_void_p(dev.ptr), a.ctypes.data_as(ctypes.c_void_p),
-                     a.nbytes, None)
-        return Binding(dev.ptr, host=a, dev=dev)
+        return _bind_host(a, _span_bytes(a))
     a = x if isinstance(x, np.ndarray) else np.asarray(x)
-    if not (a.flags.c_contiguous or a.flags.f_contiguous):
-        base = a
-        while base.base is not None and isinstance(base.base, np.ndarray):
-            base = base.base
-    n = _span_bytes(a)
-    dev = Tensor((max(n, 1),), core.uint8)
-    if n:
-        start = a.__array_interface__["data"][0]
-        hip.call("ek_memcpy_h2d", ctypes.c_void_p(dev.ptr), ctypes.c_void_p(start), n, None)
-    return Binding(dev.ptr, host=a, dev=dev)
+    return _bind_host(a, _span_bytes(a))
 
 
 def _span_bytes(a: np.ndarray) -> int:

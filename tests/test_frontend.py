@@ -149,3 +149,12 @@ def test_combine_function_errors():
         _jk("arity")
     with pytest.raises(CompilationError, match="needs an `axis`"):
         _jk("scan_axis")
+
+
+def test_capture_and_lazy_mlx_arguments():
+    with pytest.raises(ValueError, match=".json"):
+        with enceladus.capture("trace.gputrace"):
+            pass
+    enceladus.lazy_mlx(False)
+    with pytest.raises(NotImplementedError, match="MLX"):
+        enceladus.lazy_mlx(True)

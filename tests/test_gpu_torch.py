@@ -124,3 +124,62 @@ def test_device_print_lines(capfd):
     lines = [ln for ln in out.splitlines() if ln.startswith("pid (0, 0, 0) idx")]
     assert len(lines) == 64
     assert "pid (0, 0, 0) idx (3) x: 3.000000" in lines
+
+
+def test_tensor_factories():
+    import enceladus
+    print("[case] tensor factories", flush=True)
+    assert np.array_equal(enceladus.ones((2, 3)).numpy(), np.ones((2, 3), np.float32))
+    assert np.array_equal(enceladus.full(4, 7, "int32").numpy(), np.full(4, 7, np.int32))
+    assert np.array_equal(enceladus.arange(5).numpy(), np.arange(5, dtype=np.int32))
+    assert np.array_equal(enceladus.arange(2, 10, 3, dtype="int64").numpy(),
+                          np.arange(2, 10, 3, dtype=np.int64))
+    r = enceladus.rand(64, 32, seed=3).numpy()
+    assert r.shape == (64, 32) and r.min() >= 0 and r.max() < 1
+    assert np.array_equal(r, np.random.default_rng(3).random((64, 32), dtype=np.float32))
+    z = enceladus.zeros_like(enceladus.ones((8,), "float16"))
+    assert z.dtype.name == "fp16" and np.array_equal(z.numpy(), np.zeros(8, np.float16))
+    assert enceladus.empty_like(np.zeros((3, 5), np.int8)).shape == (3, 5)
+
+
+def test_async_numpy_chains_launches_and_copies_back_on_synchronize():
+    import enceladus
+    import enceladus.language as tl
+    from examples.vector_add import add_kernel
+    print("[case] async_numpy", flush=True)
+    n = 10_000
+    x = np.arange(n, dtype=np.float32)
+    y = np.ones(n, np.float32)
+    out = np.zeros(n, np.float32)
+    enceladus.async_numpy(True)
+    try:
+        grid = (enceladus.cdiv(n, 1024),)
+        add_kernel[grid](x, y, out, n, BLOCK=1024)      # out = x + 1
+        add_kernel[grid](out, y, out, n, BLOCK=1024)    # reads the pending device copy
+        enceladus.synchronize()
+        assert np.array_equal(out, x + 2)
+    finally:
+        enceladus.async_numpy(False)
+    add_kernel[grid](x, y, out, n, BLOCK=1024)          # synchronous again
+    assert np.array_equal(out, x + 1)
+
+
+def test_capture_writes_a_dispatch_trace(tmp_path):
+    import json
+
+    import torch
+
+    import enceladus
+    from examples.vector_add import add_kernel
+    print("[case] capture", flush=True)
+    x = torch.randn(1 << 20, device="cuda")
+    out = torch.empty_like(x)
+    path = tmp_path / "add.trace.json"
+    with enceladus.capture(path) as p:
+        for _ in range(3):
+            add_kernel[(1024,)](x, x, out, x.numel(), BLOCK=1024)
+    ev = json.loads(open(p).read())["traceEvents"]
+    assert len(ev) == 3 and all(e["name"] == "ek_add_kernel" for e in ev)
+    assert all(e["dur"] > 0 and e["args"]["grid"][0] == 1024 for e in ev)
+    assert ev[0]["ts"] <= ev[1]["ts"] <= ev[2]["ts"]
+    torch.testing.assert_close(out, 2 * x)
