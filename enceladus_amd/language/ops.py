@@ -720,6 +720,23 @@ F.TILE_METHODS["reshape"] = lambda ctx, x, *shape, can_reorder=False: reshape._e
 F.TILE_METHODS["broadcast_to"] = lambda ctx, x, *shape: broadcast_to._ek_frontend(
     ctx, x, *shape)
 F.TILE_METHODS["expand_dims"] = lambda ctx, x, axis: expand_dims._ek_frontend(ctx, x, axis)
+# the rest of the reference's tile methods (reference: language/ops.py:1714-1721)
+F.TILE_METHODS["permute"] = _trans
+F.TILE_METHODS["cast"] = lambda ctx, x, dtype, bitcast=False, fp_downcast_rounding=None: \
+    cast._ek_frontend(ctx, x, dtype, bitcast, fp_downcast_rounding)
+F.TILE_METHODS["abs"] = lambda ctx, x: abs_._ek_frontend(ctx, x)
+F.TILE_METHODS["sum"] = lambda ctx, x, axis=None, keep_dims=False, dtype=None: \
+    sum_._ek_frontend(ctx, x, axis, keep_dims, dtype)
+F.TILE_METHODS["max"] = lambda ctx, x, axis=None, return_indices=False, \
+    return_indices_tie_break_left=True, keep_dims=False: max_._ek_frontend(
+        ctx, x, axis, return_indices, return_indices_tie_break_left, keep_dims)
+F.TILE_METHODS["min"] = lambda ctx, x, axis=None, return_indices=False, \
+    return_indices_tie_break_left=True, keep_dims=False: min_._ek_frontend(
+        ctx, x, axis, return_indices, return_indices_tie_break_left, keep_dims)
+F.TILE_METHODS["argmax"] = lambda ctx, x, axis, tie_break_left=True, keep_dims=False: \
+    argmax._ek_frontend(ctx, x, axis, tie_break_left, keep_dims)
+F.TILE_METHODS["argmin"] = lambda ctx, x, axis, tie_break_left=True, keep_dims=False: \
+    argmin._ek_frontend(ctx, x, axis, tie_break_left, keep_dims)
 
 
 # -- dot ----------------------------------------------------------------------------

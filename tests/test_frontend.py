@@ -158,3 +158,20 @@ def test_capture_and_lazy_mlx_arguments():
     enceladus.lazy_mlx(False)
     with pytest.raises(NotImplementedError, match="MLX"):
         enceladus.lazy_mlx(True)
+
+
+@enceladus.jit
+def _methods_kernel(x_ptr, out_ptr):
+    r = tl.arange(0, 16)
+    x = tl.load(x_ptr + r[:, None] * 8 + tl.arange(0, 8)[None, :])
+    a = x.permute(1, 0).abs().cast(tl.float16)
+    v, i = x.max(axis=1, return_indices=True)
+    s = x.sum(axis=0, keep_dims=True)
+    tl.store(out_ptr + r, v + i.to(tl.float32) + tl.sum(a.to(tl.float32), 0) * 0.0 +
+             tl.sum(s) * 0.0 + x.argmin(1).to(tl.float32))
+
+
+def test_reference_tile_methods():
+    f = _methods_kernel.ir_for(np.zeros(4, np.float32), np.zeros(4, np.float32))
+    names = {op.name for op in ir.walk(f.body)}
+    assert {"trans", "unary", "cast", "reduce"} <= names
