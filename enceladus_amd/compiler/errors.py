@@ -6,14 +6,20 @@ from __future__ import annotations
 class CompilationError(Exception):
     """A kernel the compiler rejects, located at the kernel source line when known."""
 
-    def __init__(self, msg: str, loc: tuple[str, int] | None = None, src_line: str | None = None):
+    def __init__(self, msg: str, loc: tuple[str, int] | None = None, src_line: str | None = None,
+                 col: int | None = None):
         self.msg = msg
         self.loc = loc
         text = msg
         if loc is not None:
             text = f"{loc[0]}:{loc[1]}: {msg}"
             if src_line:
-                text += f"\n    {src_line.strip()}"
+                # the kernel's line as written, and a caret under the offending expression
+                line = src_line.rstrip("\n").rstrip()
+                text += f"\n{line}"
+                if col is None:
+                    col = len(line) - len(line.lstrip())
+                text += "\n" + " " * col + "^"
         super().__init__(text)
 
 

@@ -35,8 +35,9 @@ _PY_BIN = {"add": lambda a, b: a + b, "sub": lambda a, b: a - b, "mul": lambda a
 
 
 class _Return(Exception):
-    def __init__(self, value):
+    def __init__(self, value, node=None):
         self.value = value
+        self.node = node
 
 
 class BoundMethod:
@@ -112,7 +113,8 @@ class CodeGenerator(ast.NodeVisitor):
         src = None
         if 0 < getattr(node, "lineno", 0) <= len(self.src_lines):
             src = self.src_lines[node.lineno - 1]
-        return CompilationError(msg, (self.filename, line), src)
+        return CompilationError(msg, (self.filename, line), src,
+                                getattr(node, "col_offset", None))
 
     def visit(self, node):
         if isinstance(node, ast.stmt):
@@ -188,7 +190,7 @@ class CodeGenerator(ast.NodeVisitor):
         self.scope[node.target.id] = self.binop(_BINOPS[type(node.op)], cur, rhs, node)
 
     def visit_Return(self, node):
-        raise _Return(None if node.value is None else self.visit(node.value))
+        raise _Return(None if node.value is None else self.visit(node.value), node)
 
     def visit_Assert(self, node):
         cond = self.visit(node.test)
@@ -206,7 +208,8 @@ class CodeGenerator(ast.NodeVisitor):
             self.visit_stmts(node.body if cond else node.orelse)
             return
         if cond.type.shape != ():
-            raise self.error(node, "`if` needs a scalar condition")
+            raise self.error(node, "`if` needs a scalar condition; for a tile condition use "
+                                   "tl.where(cond, a, b)")
         self.runtime_if(node, cond)
 
     def _names_assigned(self, stmts) -> list[str]:
@@ -355,6 +358,11 @@ class CodeGenerator(ast.NodeVisitor):
             if not is_value(before) and not is_value(after):
                 if core.unwrap(before) == core.unwrap(after):
                     continue
+            if is_value(before) and is_value(after) and after.type != before.type:
+                raise self.error(
+                    node, f"loop-carried variable `{n}` has type {before.type} before the loop "
+                          f"but {after.type} at the end of the body. Convert it with `.to(...)` "
+                          "so that the type stays the same, or initialize it with the final type.")
             names.append(n)
             bv = before
             if not is_value(bv):
@@ -402,6 +410,17 @@ class CodeGenerator(ast.NodeVisitor):
                       attrs, regions=[body])
         for n, r in zip(names, op.results):
             self.scope[n] = r
+        # As in Python, the loop variable keeps its last value after the loop, or its value
+        # from before the loop when the loop doesn't run.
+        span = semantic.binary(b, "sub", semantic.binary(b, "sub", hi_v, lo_v), 1)
+        last = semantic.binary(b, "add", lo_v, semantic.binary(
+            b, "mul", semantic.binary(b, "floordiv", span, step_v), step_v))
+        prior = self.scope.get(iv_name)
+        if prior is not None and (not is_value(core.unwrap(prior)) or
+                                  core.unwrap(prior).type.shape == ()):
+            ran = semantic.binary(b, "lt", lo_v, hi_v)
+            last = semantic.select(b, ran, last, prior)
+        self.scope[iv_name] = last
 
     def visit_While(self, node):
         raise self.error(node, "`while` loops aren't supported; use `for ... in range(...)`")
@@ -529,10 +548,27 @@ class CodeGenerator(ast.NodeVisitor):
         if not is_value(a) and not is_value(b_):
             return (a and b_) if kind == "and" else (a or b_)
         op = "and" if kind == "and" else "or"
-        for v in (a, b_):
-            if is_value(v) and not v.type.dtype.is_bool():
-                raise CompilationError(f"`{kind}` on tiles needs boolean operands; use & or |")
-        return semantic.binary(self.b, op, a, b_)
+        if all(not is_value(v) or v.type.dtype.is_bool() for v in (a, b_)):
+            return semantic.binary(self.b, op, a, b_)
+        if any(is_value(v) and v.type.shape for v in (a, b_)):
+            raise CompilationError(f"`{kind}` on tiles needs boolean operands; use & or |")
+        # Python's value semantics on runtime scalars: `a or b` is a when a is truthy, else
+        # b; `a and b` is a when a is falsy, else b. Both sides must share a type.
+        ta = a.type.dtype if is_value(a) else None
+        tb = b_.type.dtype if is_value(b_) else None
+        dt = ta or tb
+        for v, t in ((a, ta), (b_, tb)):
+            if t is None and semantic.adopt_literal(v, dt) is not dt:
+                t = semantic.literal_dtype(v)
+            if (t or dt) is not dt:
+                raise CompilationError(
+                    f"`{kind}` of {ta or semantic.literal_dtype(a)} and "
+                    f"{tb or semantic.literal_dtype(b_)}: both need the same type (Python would "
+                    "return either one); convert one side with `.to(...)`")
+        av, bv = semantic.to_value(self.b, a, dt), semantic.to_value(self.b, b_, dt)
+        truthy = semantic.binary(self.b, "ne", av, 0)
+        return semantic.select(self.b, truthy, av, bv) if kind == "or" else \
+            semantic.select(self.b, truthy, bv, av)
 
     def visit_BoolOp(self, node):
         kind = "and" if isinstance(node.op, ast.And) else "or"
@@ -609,6 +645,18 @@ def inline_jit(ctx: Context, jfn, args, kwargs=None):
     """Emits the body of the @jit function `jfn` called with `args` at the builder's
     current position and returns its return value (a tuple for several values)."""
     fn = jfn.fn
+    stack = ctx.__dict__.setdefault("inlining", [])
+    if fn in stack:
+        raise _BadCall(f"recursion isn't supported: `{fn.__name__}` calls itself (through "
+                       f"{' -> '.join(f.__name__ for f in stack)})")
+    stack.append(fn)
+    try:
+        return _inline(ctx, fn, args, kwargs)
+    finally:
+        stack.pop()
+
+
+def _inline(ctx: Context, fn, args, kwargs):
     sig = inspect.signature(fn)
     try:
         bound = sig.bind(*args, **(kwargs or {}))
@@ -735,5 +783,8 @@ def build_ir(fn, arg_types: dict[str, Any], arg_facts: dict[str, dict], constexp
         gen.visit_stmts(fdef.body)
     except _Return as r:
         if r.value is not None:
+            if r.node is not None:
+                raise gen.error(r.node, "kernels can't return values; store results through "
+                                        "a pointer argument") from None
             raise CompilationError("kernels can't return values") from None
     return ir.Func(fn.__name__, args, names, body, num_warps, dict(options or {}))

@@ -175,3 +175,62 @@ def test_reference_tile_methods():
     f = _methods_kernel.ir_for(np.zeros(4, np.float32), np.zeros(4, np.float32))
     names = {op.name for op in ir.walk(f.body)}
     assert {"trans", "unary", "cast", "reduce"} <= names
+
+
+# -- source-located errors (reference strategy: tests/test_frontend.py:24-109) -----------
+
+@enceladus.jit
+def _e_loop_type(x_ptr, n, BLOCK: tl.constexpr):
+    acc = tl.zeros((BLOCK,), dtype=tl.float32)
+    for _ in range(n):  # error
+        acc = (acc + 1.0).to(tl.float16)
+    tl.store(x_ptr + tl.arange(0, BLOCK), acc)
+
+
+@enceladus.jit
+def _e_or_types(x_ptr, n):
+    tl.store(x_ptr, n or 2.5)  # error
+
+
+@enceladus.jit
+def _e_returns(x_ptr):
+    return tl.load(x_ptr)  # error
+
+
+@enceladus.jit
+def _e_rec(x):
+    return _e_rec(x)  # error
+
+
+@enceladus.jit
+def _e_calls_rec(x_ptr):
+    tl.store(x_ptr, _e_rec(1.0))
+
+
+@enceladus.jit
+def _e_if_tile(x_ptr, BLOCK: tl.constexpr):
+    x = tl.load(x_ptr + tl.arange(0, BLOCK))
+    if x > 0:  # error
+        x = -x
+    tl.store(x_ptr + tl.arange(0, BLOCK), x)
+
+
+@pytest.mark.parametrize("kernel,args,kw,phrase", [
+    (_e_loop_type, (64,), {"BLOCK": 64}, "loop-carried variable `acc`"),
+    (_e_or_types, (64,), {}, "both need the same type"),
+    (_e_returns, (), {}, "can't return values"),
+    (_e_calls_rec, (), {}, "recursion isn't supported"),
+    (_e_if_tile, (), {"BLOCK": 64}, "tl.where"),
+])
+def test_errors_point_at_the_marked_line(kernel, args, kw, phrase):
+    import inspect
+    with pytest.raises(CompilationError) as e:
+        kernel.ir_for(np.zeros(64, np.float32), *args, **kw)
+    msg = str(e.value)
+    assert phrase in msg
+    fn = _e_rec.fn if kernel is _e_calls_rec else kernel.fn
+    lines, start = inspect.getsourcelines(fn)
+    off = next(i for i, t in enumerate(lines) if t.rstrip().endswith("# error"))
+    assert f"{__file__}:{start + off}:" in msg
+    assert lines[off].rstrip() in msg.splitlines()
+    assert msg.splitlines()[-1].strip() == "^"

@@ -227,3 +227,85 @@ def test_matmul_template_bf16_torch():
     c = matmul_desc(a.cuda(), b.cuda(), bm=256, bn=256, bk=64).float().cpu()
     want = (a.float() @ b.float()).bfloat16().float()
     np.testing.assert_allclose(c.numpy(), want.numpy(), rtol=1.6e-2, atol=1e-2)
+
+
+# -- Python semantics in compiled kernels (reference: tests/test_frontend.py:112-193) -----
+
+import enceladus.language as tl  # noqa: E402
+
+
+@enceladus.jit
+def _loop_var_after_loop(out_ptr, n):
+    i = 100
+    for i in range(n):  # noqa: B007 - `i` is read after the loop
+        pass
+    tl.store(out_ptr, i)
+
+
+@enceladus.jit
+def _negate_mask(out_ptr, x_ptr, BLOCK: tl.constexpr):
+    offs = tl.arange(0, BLOCK)
+    m = tl.load(x_ptr + offs) > 0
+    tl.store(out_ptr + offs, -m + 10 * ~m)
+
+
+@enceladus.jit
+def _unsigned_loop_bound(out_ptr, n_ptr):
+    n = tl.load(n_ptr)
+    count = 0
+    for _ in range(0, n, 1_000_000_000):
+        count += 1
+    tl.store(out_ptr, count)
+
+
+@enceladus.jit
+def _chained_compare(out_ptr, x_ptr, a, b):
+    tl.store(out_ptr, (a < b <= tl.load(x_ptr)).to(tl.int32))
+
+
+@enceladus.jit
+def _where_pointers(out_ptr, x_ptr, BLOCK: tl.constexpr):
+    offs = tl.arange(0, BLOCK)
+    tl.store(out_ptr + offs, tl.load(tl.where(offs % 2 == 0, x_ptr + offs, x_ptr + 50 + offs)))
+
+
+@enceladus.jit
+def _scalar_or(out_ptr, a, b):
+    tl.store(out_ptr, a or b)
+    tl.store(out_ptr + 1, a and b)
+
+
+_VALS = np.arange(-32, 96, dtype=np.int32)
+
+
+@pytest.mark.parametrize("case", ["loop_after", "loop_empty", "negate_mask", "uint_bound",
+                                  "chained", "chained_short", "where_ptrs", "or_and",
+                                  "or_and_zero"])
+def test_python_semantics(case):
+    _say(f"semantics {case}")
+    i32 = np.zeros(2, np.int32)
+    if case == "loop_after":
+        _loop_var_after_loop[(1,)](i32, 5)
+        assert i32[0] == 4
+    elif case == "loop_empty":
+        _loop_var_after_loop[(1,)](i32, 0)
+        assert i32[0] == 100
+    elif case == "negate_mask":
+        out = np.zeros(64, np.int32)
+        _negate_mask[(1,)](out, _VALS, BLOCK=64)
+        assert np.array_equal(out, np.where(_VALS[:64] > 0, -1, 10))
+    elif case == "uint_bound":
+        _unsigned_loop_bound[(1,)](i32, np.array([3_000_000_000], np.uint32))
+        assert i32[0] == 3
+    elif case in ("chained", "chained_short"):
+        a, b = (1, 2) if case == "chained" else (3, 2)
+        _chained_compare[(1,)](i32, _VALS[40:], a, b)
+        assert i32[0] == (1 if case == "chained" else 0)
+    elif case == "where_ptrs":
+        out = np.zeros(64, np.int32)
+        _where_pointers[(1,)](out, _VALS, BLOCK=64)
+        assert np.array_equal(out, np.where(np.arange(64) % 2 == 0, _VALS[:64], _VALS[50:114]))
+    else:
+        a = 0 if case == "or_and_zero" else 6
+        _scalar_or[(1,)](i32, a, 9)
+        assert list(i32) == [a or 9, a and 9]
