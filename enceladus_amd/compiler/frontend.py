@@ -34,6 +34,13 @@ _PY_BIN = {"add": lambda a, b: a + b, "sub": lambda a, b: a - b, "mul": lambda a
            "le": lambda a, b: a <= b, "gt": lambda a, b: a > b, "ge": lambda a, b: a >= b}
 
 
+class _Poison:
+    """A name whose value can't be used (reading it raises the stored error)."""
+
+    def __init__(self, msg: str):
+        self.msg = msg
+
+
 class _Return(Exception):
     def __init__(self, value, node=None):
         self.value = value
@@ -134,7 +141,13 @@ class CodeGenerator(ast.NodeVisitor):
             raise
 
     def generic_visit(self, node):
-        raise self.error(node, f"unsupported syntax: {type(node).__name__} (`{_unparse(node)}`)")
+        hint = ""
+        if isinstance(node, (ast.Dict, ast.Set, ast.DictComp, ast.SetComp)):
+            hint = ". Use a compile-time tuple, or pass values as tl.constexpr arguments."
+        elif isinstance(node, ast.Lambda):
+            hint = ". Define an @enceladus.jit function instead."
+        raise self.error(node, f"unsupported syntax: {type(node).__name__} "
+                               f"(`{_unparse(node)}`){hint}")
 
     # -- statements ----------------------------------------------------------
     def visit_stmts(self, stmts):
@@ -415,11 +428,20 @@ class CodeGenerator(ast.NodeVisitor):
         span = semantic.binary(b, "sub", semantic.binary(b, "sub", hi_v, lo_v), 1)
         last = semantic.binary(b, "add", lo_v, semantic.binary(
             b, "mul", semantic.binary(b, "floordiv", span, step_v), step_v))
-        prior = self.scope.get(iv_name)
-        if prior is not None and (not is_value(core.unwrap(prior)) or
-                                  core.unwrap(prior).type.shape == ()):
-            ran = semantic.binary(b, "lt", lo_v, hi_v)
-            last = semantic.select(b, ran, last, prior)
+        prior = core.unwrap(self.scope.get(iv_name))
+        if prior is not None:
+            pdt = prior.type.dtype if is_value(prior) and not isinstance(prior.type, ir.DescType) \
+                else None
+            same = (pdt is dt and prior.type.shape == ()) if is_value(prior) else (
+                isinstance(prior, int) and not isinstance(prior, bool) and
+                semantic.adopt_literal(prior, dt) is dt)
+            if same:
+                ran = semantic.binary(b, "lt", lo_v, hi_v)
+                last = semantic.select(b, ran, last, prior)
+            else:
+                last = _Poison(f"`{iv_name}` is {prior!r} before the loop and an integer loop "
+                               "counter inside it, so its type after the loop depends on "
+                               "whether the loop ran. Give the loop variable a different name.")
         self.scope[iv_name] = last
 
     def visit_While(self, node):
@@ -434,7 +456,10 @@ class CodeGenerator(ast.NodeVisitor):
     # -- expressions ---------------------------------------------------------
     def lookup(self, name: str, node):
         if name in self.scope:
-            return self.scope[name]
+            v = self.scope[name]
+            if isinstance(v, _Poison):
+                raise self.error(node, v.msg)
+            return v
         if name in self.globals:
             v = self.globals[name]
             return v
@@ -501,6 +526,12 @@ class CodeGenerator(ast.NodeVisitor):
         a = self.visit(node.left)
         b_ = self.visit(node.right)
         if type(node.op) not in _BINOPS:
+            if isinstance(node.op, ast.Pow):
+                ca, cb = core.unwrap(a), core.unwrap(b_)
+                if not is_value(ca) and not is_value(cb):
+                    return ca ** cb
+                raise self.error(node, "`**` isn't supported on runtime values. Multiply "
+                                       "explicitly (`x * x`), or use tl.exp2/tl.log2.")
             raise self.error(node, f"unsupported operator {type(node.op).__name__}")
         return self.binop(_BINOPS[type(node.op)], a, b_, node)
 
@@ -539,6 +570,9 @@ class CodeGenerator(ast.NodeVisitor):
                     c = not c
             else:
                 c = self.binop(_CMPOPS[type(op)], left, right, node)
+            if result is not None and is_value(core.unwrap(c)) and core.unwrap(c).type.shape:
+                raise self.error(node, "chained comparisons on tiles have no single truth "
+                                       "value in Python. Write `(a < b) & (b < c)`.")
             result = c if result is None else self.logical("and", result, c)
             left = right
         return result
@@ -548,10 +582,12 @@ class CodeGenerator(ast.NodeVisitor):
         if not is_value(a) and not is_value(b_):
             return (a and b_) if kind == "and" else (a or b_)
         op = "and" if kind == "and" else "or"
+        if any(is_value(v) and v.type.shape for v in (a, b_)):
+            sym = "&" if kind == "and" else "|"
+            raise CompilationError(f"`{kind}` on tiles has no single truth value in Python; "
+                                   f"use `{sym}` for the elementwise {kind} of masks")
         if all(not is_value(v) or v.type.dtype.is_bool() for v in (a, b_)):
             return semantic.binary(self.b, op, a, b_)
-        if any(is_value(v) and v.type.shape for v in (a, b_)):
-            raise CompilationError(f"`{kind}` on tiles needs boolean operands; use & or |")
         # Python's value semantics on runtime scalars: `a or b` is a when a is truthy, else
         # b; `a and b` is a when a is falsy, else b. Both sides must share a type.
         ta = a.type.dtype if is_value(a) else None
@@ -624,6 +660,10 @@ class CodeGenerator(ast.NodeVisitor):
                 return semantic.cast(self.b, core.unwrap(args[0]), core.int32)
             if fn is builtins.abs:
                 return semantic.unary(self.b, "abs", core.unwrap(args[0]))
+            if fn is builtins.print:
+                raise self.error(node, "`print` runs when the kernel compiles and can't show "
+                                       "runtime values. Use tl.device_print (or "
+                                       "tl.static_print for compile-time values).")
             raise self.error(node, f"`{getattr(fn, '__name__', fn)}` can't take runtime values")
         if fn is builtins.print:
             return None

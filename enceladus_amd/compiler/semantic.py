@@ -157,7 +157,9 @@ def coerce_literal(v, dt: core.dtype):
     if lo <= v <= hi:
         return v
     if not -(1 << (bits - 1)) <= v < (1 << bits):
-        raise CompilationError(f"the value {v} doesn't fit in {dt}")
+        raise CompilationError(f"the value {v} doesn't fit in {dt}. Use a value in that range "
+                               f"[{lo}, {hi}], or convert the {dt} operand with "
+                               "`.to(tl.int32)` (or a wider type) first.")
     v &= (1 << bits) - 1
     if dt.is_signed() and v >> (bits - 1):
         v -= 1 << bits

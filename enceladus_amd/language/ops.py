@@ -41,7 +41,12 @@ def builtin(name: str | None = None):
 
 def _cint(v: Any, what: str) -> int:
     v = core.unwrap(v)
-    if isinstance(v, ir.Value) or isinstance(v, bool) or not isinstance(v, int):
+    if isinstance(v, ir.Value):
+        nm = v.name_hint or "it"
+        raise CompilationError(
+            f"{what} must be a compile-time integer, but `{nm}` is a runtime value. If it is "
+            f"a kernel parameter, annotate it as `{nm}: tl.constexpr`.")
+    if isinstance(v, bool) or not isinstance(v, int):
         raise CompilationError(f"{what} must be a compile-time integer, but got {v!r}")
     return v
 
@@ -102,7 +107,8 @@ def arange(ctx, start, end):
     n = e - s
     if n <= 0 or n & (n - 1) or n > ir.MAX_TILE_NUMEL:
         raise CompilationError(f"arange({s}, {e}) must have a power-of-two length "
-                               f"<= {ir.MAX_TILE_NUMEL}")
+                               f"<= {ir.MAX_TILE_NUMEL}. Round the block size up to a power "
+                               "of two and mask the extra elements.")
     return ctx.b.create("arange", [], [ir.TType((n,), core.int32)], {"start": s}).result
 
 
@@ -784,7 +790,8 @@ def dot(ctx, input, other, acc=None, input_precision=None, allow_tf32=None,
         if adt.primitive_bitwidth not in (8, 16, 32) or adt.is_bool():
             raise CompilationError(f"tl.dot takes 8-, 16- or 32-bit integer operands, got {adt}")
         if out_dt is not core.int32:
-            raise CompilationError("tl.dot accumulates integer operands in int32")
+            raise CompilationError("tl.dot accumulates integer operands in int32; create the "
+                                   "accumulator with `tl.zeros(..., dtype=tl.int32)`")
         if a.type.shape[1] % 8:
             raise CompilationError(f"tl.dot needs a K dimension that is a multiple of 8, got "
                                    f"{a.type.shape[1]}")
@@ -811,7 +818,8 @@ def _atomic(ctx, kind, pointer, vals, mask, sem, scope):
     if dt.is_floating() and kind in _ATOMIC_BITWISE:
         raise CompilationError(f"tl.atomic_{kind} needs integer elements")
     if kind == "add" and dt in (core.float16, core.bfloat16):
-        raise CompilationError(f"tl.atomic_add doesn't support {dt}")
+        raise CompilationError(f"tl.atomic_add doesn't support {dt}. Accumulate in a float32 "
+                               "buffer and convert the result afterwards.")
     if dt.primitive_bitwidth == 64 and not (dt is core.uint64 and kind in ("max", "min")):
         raise CompilationError(f"tl.atomic_{kind} doesn't support {dt}")
     vs = [semantic.to_value(b, v, dt) for v in vals]

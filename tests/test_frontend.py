@@ -234,3 +234,74 @@ def test_errors_point_at_the_marked_line(kernel, args, kw, phrase):
     assert f"{__file__}:{start + off}:" in msg
     assert lines[off].rstrip() in msg.splitlines()
     assert msg.splitlines()[-1].strip() == "^"
+
+
+@enceladus.jit
+def _h_constexpr(x_ptr, BLOCK):
+    tl.store(x_ptr + tl.arange(0, BLOCK), 1.0)  # error
+
+
+@enceladus.jit
+def _h_and_tiles(x_ptr, BLOCK: tl.constexpr):
+    x = tl.load(x_ptr + tl.arange(0, BLOCK))
+    tl.store(x_ptr + tl.arange(0, BLOCK), x, mask=(x > 0) and (x < 1))  # error
+
+
+@enceladus.jit
+def _h_pow(x_ptr, BLOCK: tl.constexpr):
+    x = tl.load(x_ptr + tl.arange(0, BLOCK))
+    tl.store(x_ptr + tl.arange(0, BLOCK), x**2)  # error
+
+
+@enceladus.jit
+def _h_print(x_ptr, BLOCK: tl.constexpr):
+    x = tl.load(x_ptr + tl.arange(0, BLOCK))
+    print(x)  # error
+
+
+@enceladus.jit
+def _h_loopvar(x_ptr, n):
+    i = 0.5
+    for i in range(n):  # noqa: B007
+        pass
+    tl.store(x_ptr, i)  # error
+
+
+@enceladus.jit
+def _h_chained(x_ptr, BLOCK: tl.constexpr):
+    x = tl.load(x_ptr + tl.arange(0, BLOCK))
+    tl.store(x_ptr + tl.arange(0, BLOCK), x, mask=0 < x < 1)  # error
+
+
+@enceladus.jit
+def _h_dict(x_ptr):
+    scale = {"a": 2.0}  # error
+    tl.store(x_ptr, scale["a"])
+
+
+@enceladus.jit
+def _h_full_range(x_ptr, BLOCK: tl.constexpr):
+    tl.store(x_ptr + tl.arange(0, BLOCK), tl.full((BLOCK,), 1e10, tl.int32))  # error
+
+
+@pytest.mark.parametrize("kernel,args,kw,phrase", [
+    (_h_constexpr, (16,), {}, "`BLOCK: tl.constexpr`"),
+    (_h_and_tiles, (), {"BLOCK": 16}, "use `&`"),
+    (_h_pow, (), {"BLOCK": 16}, "Multiply explicitly"),
+    (_h_print, (), {"BLOCK": 16}, "Use tl.device_print"),
+    (_h_loopvar, (3,), {}, "Give the loop variable a different name"),
+    (_h_chained, (), {"BLOCK": 16}, "`(a < b) & (b < c)`"),
+    (_h_dict, (), {}, "Use a compile-time tuple"),
+    (_h_full_range, (), {"BLOCK": 16}, "Use a value in that range"),
+])
+def test_errors_say_what_to_do(kernel, args, kw, phrase):
+    """Each error names the marked line and the fix (reference: tests/test_errors.py:24-271)."""
+    import inspect
+    x = np.zeros(64, np.int32 if kernel is _h_full_range else np.float32)
+    with pytest.raises(CompilationError) as e:
+        kernel.ir_for(x, *args, **kw)
+    msg = str(e.value)
+    assert phrase in msg
+    lines, start = inspect.getsourcelines(kernel.fn)
+    off = next(i for i, t in enumerate(lines) if t.rstrip().endswith("# error"))
+    assert f"{__file__}:{start + off}:" in msg
