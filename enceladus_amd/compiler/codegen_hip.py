@@ -280,11 +280,11 @@ class Emitter:
             try:
                 base[d] = LY.plan_dot(a.type.shape[0], b.type.shape[1], a.type.shape[1],
                                       self.nw, adt.name, dw)
-            except ValueError as e:
-                if adt.is_int():
-                    self.int_dots.add(d.result.id)
-                    continue
-                raise CompilationError(str(e)) from None
+            except ValueError:
+                # tiles below the MFMA minimums (16x16, K a multiple of the instruction
+                # depth): multiply-adds from LDS
+                self.int_dots.add(d.result.id)
+                continue
             dots.append(d)
         trans, korder = set(), {}
         if not self.opt.get("no_dot_transpose"):
@@ -1950,11 +1950,13 @@ class Emitter:
                   f"&{sm}[{idx}]);")
 
     def op_dot_int(self, op):
-        """Integer product without MFMA (uint8, 16- and 32-bit operands, or tiles the i8
-        MFMAs can't take): both operands go to LDS as int32 (A rows padded by one word so
-        a wave's different rows hit different banks), then every thread accumulates its
-        own outputs over k. Arithmetic is unsigned 32-bit, so products and sums wrap
-        modulo 2^32 as the integer tl.dot defines."""
+        """A product without MFMA: integer operands other than int8 (uint8, 16- and 32-bit),
+        and tiles below the MFMA minimums (an 8x8 tile, K = 8 with 16-bit floats). Both
+        operands go to LDS as 32-bit values (int32, or fp32 for floats; A rows padded by one
+        word so a wave's different rows hit different banks), then every thread accumulates
+        its own outputs over k: integers in unsigned 32-bit arithmetic, so products and sums
+        wrap modulo 2^32 as the integer tl.dot defines; floats with fp32 fma, rounded to the
+        accumulator's dtype at the end."""
         a, b, c = op.operands
         res = op.result
         lay = self.lay[res.id]
@@ -1965,29 +1967,44 @@ class Emitter:
         la = self.lay[a.id] if self.kind.get(a.id) == "anchored" else self.default_layout(a)
         lb = self.lay[b.id] if self.kind.get(b.id) == "anchored" else self.default_layout(b)
         xa, xb = self.array(a, la), self.array(b, lb)
+        flt = a.type.dtype.is_floating()
+        T = "float" if flt else "int32_t"
+        cvt = (lambda x: f"ek::f32({x})") if flt else (lambda x: f"(int32_t){x}")
         nm = self.fresh("acc")
-        self.emit(f"int32_t {nm}[{lay.nregs}];")
+        self.emit(f"{T} {nm}[{lay.nregs}];")
         self.emit("#pragma unroll")
         self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = "
-                  f"(int32_t)({self.elem(c, lay, 'r')});")
+                  f"{cvt('(' + self.elem(c, lay, 'r') + ')')};")
         mr, nr = self.coord(lay, 0, "r"), self.coord(lay, 1, "r")
         self.emit("{")
-        self.emit("  int32_t* sa = reinterpret_cast<int32_t*>(ek_smem);")
-        self.emit(f"  int32_t* sb = sa + {M * pa};")
+        self.emit(f"  {T}* sa = reinterpret_cast<{T}*>(ek_smem);")
+        self.emit(f"  {T}* sb = sa + {M * pa};")
         self.emit("  __syncthreads();")
         self.emit("  #pragma unroll")
         self.emit(f"  for (int r = 0; r < {la.nregs}; ++r) sa[({self.coord(la, 0, 'r')}) * "
-                  f"{pa} + ({self.coord(la, 1, 'r')})] = (int32_t){xa}[r];")
+                  f"{pa} + ({self.coord(la, 1, 'r')})] = {cvt(xa + '[r]')};")
         self.emit("  #pragma unroll")
         self.emit(f"  for (int r = 0; r < {lb.nregs}; ++r) sb[({self.coord(lb, 0, 'r')}) * "
-                  f"{N} + ({self.coord(lb, 1, 'r')})] = (int32_t){xb}[r];")
+                  f"{N} + ({self.coord(lb, 1, 'r')})] = {cvt(xb + '[r]')};")
         self.emit("  __syncthreads();")
         self.emit(f"  for (int k = 0; k < {K}; ++k) {{")
         self.emit("    #pragma unroll")
-        self.emit(f"    for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = (int32_t)((uint32_t){nm}[r]"
-                  f" + (uint32_t)sa[({mr}) * {pa} + k] * (uint32_t)sb[k * {N} + ({nr})]);")
+        ea, eb = f"sa[({mr}) * {pa} + k]", f"sb[k * {N} + ({nr})]"
+        if flt:
+            self.emit(f"    for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = "
+                      f"__builtin_fmaf({ea}, {eb}, {nm}[r]);")
+        else:
+            self.emit(f"    for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = (int32_t)("
+                      f"(uint32_t){nm}[r] + (uint32_t){ea} * (uint32_t){eb});")
         self.emit("  }")
         self.emit("}")
+        cdt = res.type.dtype
+        if flt and cdt is not core.float32:
+            out = self.fresh("acch")
+            self.emit(f"{ctype(cdt)} {out}[{lay.nregs}];")
+            self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {out}[r] = ek::rnd<{ctype(cdt)}>"
+                      f"({nm}[r]);")
+            nm = out
         self.define(res, nm)
 
     def op_dot(self, op):
