@@ -184,3 +184,42 @@ def print_func(fn: Func) -> str:
     block(fn.body, 1)
     lines.append("}")
     return "\n".join(lines)
+
+
+# ops without side effects: removable when nothing reads their results
+PURE_OPS = frozenset(["const", "binary", "unary", "cast", "bitcast", "select", "splat",
+                      "broadcast", "expand_dims", "reshape", "trans", "hint", "arange",
+                      "program_id", "num_programs", "fma", "ptr_add", "join", "split",
+                      "shift"])
+
+
+def dce(fn: Func) -> int:
+    """Removes pure ops whose results nothing reads (e.g. a loop variable's after-loop
+    value that the kernel never uses). Returns how many ops were removed."""
+    used: dict[int, int] = {}
+
+    def count(b: Block):
+        for op in b.ops:
+            for o in op.operands:
+                used[o.id] = used.get(o.id, 0) + 1
+            for r in op.regions:
+                count(r)
+    count(fn.body)
+    removed = 0
+
+    def sweep(b: Block):
+        nonlocal removed
+        keep = []
+        for op in reversed(b.ops):
+            for r in op.regions:
+                sweep(r)
+            if op.name in PURE_OPS and not op.regions and op.results and \
+                    all(used.get(r.id, 0) == 0 for r in op.results):
+                for o in op.operands:
+                    used[o.id] -= 1
+                removed += 1
+                continue
+            keep.append(op)
+        b.ops = keep[::-1]
+    sweep(fn.body)
+    return removed

@@ -200,4 +200,5 @@ def build_module(jfn, arg_types, arg_facts, constexprs, num_warps, options) -> i
     fn = frontend.build_ir(jfn.fn, arg_types, arg_facts, constexprs, num_warps, options)
     if widen.needs_idx64(fn):
         widen.widen_index_math(fn)
+    ir.dce(fn)
     return fn

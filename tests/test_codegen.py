@@ -23,7 +23,7 @@ def test_codegen_is_deterministic():
     a = codegen_hip.generate(add_kernel.ir_for(x, x, x, 1000, BLOCK=256)).source
     b = codegen_hip.generate(add_kernel.ir_for(x, x, x, 1000, BLOCK=256)).source
     assert a == b
-    assert "vload<float, 4>" in a      # 128-bit accesses for aligned contiguous fp32
+    assert "vload_nt<float, 4>" in a   # 128-bit streaming accesses for aligned contiguous fp32
 
 
 def _covers_once(lay):
