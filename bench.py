@@ -64,23 +64,19 @@ def make_launch(jfn, grid, args, num_warps=4, dot_warps=None, **constexprs):
     for n in lc.runtime_names:
         v = vals[n]
         packed.append(v.data_ptr() if hasattr(v, "data_ptr") else v)
-    kern = lc.ck.pack(packed)
-    g, extra = lc.ck.launch_grid(grid)
-    if extra:
-        kern = kern + extra
-        kern += b"\0" * ((-len(kern)) % 8)
-    buf = ctypes.create_string_buffer(kern, len(kern))
-    fn = lc.ck.function()
-    blk = lc.ck.gen.block
+    import torch
+    sid = int(torch.cuda.current_stream().cuda_stream)
+    # the kernel's dispatches (a privatised histogram adds its second flush level)
+    disp = lc.ck.prepare(grid, lc.ck.pack(packed), sid)
     lib = hip.load_library()
     err = ctypes.create_string_buffer(256)
-    import torch
-    stream = ctypes.c_void_p(int(torch.cuda.current_stream().cuda_stream) or None)
+    stream = ctypes.c_void_p(sid or None)
 
     def launch():
-        rc = lib.ek_launch(stream, fn, g[0], g[1], g[2], blk, 1, 1, 0, buf, len(kern), err, 256)
-        if rc:
-            raise RuntimeError(err.value.decode())
+        for fn, g, blk, buf, n in disp:
+            rc = lib.ek_launch(stream, fn, g[0], g[1], g[2], blk, 1, 1, 0, buf, n, err, 256)
+            if rc:
+                raise RuntimeError(err.value.decode())
     launch.ck = lc.ck
     return launch
 

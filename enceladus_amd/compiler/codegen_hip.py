@@ -140,6 +140,9 @@ class GeneratedKernel:
     block: int
     coarsen: int = 0       # workgroups per CU of a coarsened launch (0: one per program)
     asserts: list = field(default_factory=list)   # tl.device_assert sites (message, loc)
+    # two-level histogram flush: {"name", "rb", "bases" (arg indices), "total" (words per
+    # workgroup row of the partial buffer)}; the launcher runs `name` after the kernel
+    flush: dict | None = None
 
 
 class Emitter:
@@ -2940,6 +2943,21 @@ class Emitter:
         if self.asserts:
             params.append("uint32_t* ek_assert_buf")
             args.append(KernelArg("ek_assert_buf", "ptr", core.uint32, "uint32_t*"))
+        # Two-level flush of privatised bins: each workgroup stores its bins to a partial
+        # buffer row (plain stores), and a second kernel sums RB rows at a time and adds each
+        # sum with one global atomic. Measured on the 1024-bin histogram: 71 -> 56 us; one
+        # global atomic per bin per workgroup (2,048 per address) cost about 29 us.
+        two = bool(self.priv) and bool(self.coarsen) and self.priv_copies == 1 and \
+            self.opt.get("priv_flush", "two_level") != "atomic" and \
+            all(i["dt"].primitive_bitwidth == 32 for i in self.priv.values())
+        if two:
+            off = 0
+            for info in self.priv.values():
+                info["off"] = off
+                off += (info["bins"] + 3) // 4 * 4
+            total_words = off
+            params.append("int32_t* __restrict__ ek_part")
+            args.append(KernelArg("ek_part", "ptr", core.int32, "int32_t*"))
         if self.coarsen:
             params += ["int32_t ek_np_x", "int32_t ek_np_y", "int32_t ek_np_z"]
         out = ['#include "enceladus_cdna4.h"', ""]
@@ -3018,7 +3036,13 @@ class Emitter:
             out.append("  }")
         else:
             out.extend(body)
-        if self.priv:
+        if two:
+            out.append("  __syncthreads();")
+            for info in self.priv.values():
+                out.append(f"  for (int i = ek_tid; i < {info['bins']}; i += {self.nt}) "
+                           f"ek_part[(size_t)blockIdx.x * {total_words} + {info['off']} + i] = "
+                           f"(int32_t){info['name']}[i];")
+        elif self.priv:
             # Flush: a wave reads consecutive words (whole groups of C copies), sums each group
             # with butterfly shuffles and one lane adds the bin's total to global memory.
             out.append("  __syncthreads();")
@@ -3037,9 +3061,38 @@ class Emitter:
                            "__HIP_MEMORY_SCOPE_AGENT);")
                 out.append("  }")
         out.append("}")
+        flush = None
+        if two:
+            rb = int(self.opt.get("priv_flush_rows", 32))
+            fname = f"{kname}_flush"
+            hs = [f"{ctype(i['dt'])}* ek_h{k}" for k, i in enumerate(self.priv.values())]
+            out += ["", "// Second level of the privatised-bin flush: workgroup x sums partial rows",
+                    f"// [x*{rb}, x*{rb}+{rb}) with 16-byte loads and adds each non-zero sum to the "
+                    "kernel's bins.",
+                    f'extern "C" __global__ void __launch_bounds__(256) {fname}('
+                    "const int32_t* __restrict__ ek_part, int32_t ek_nwg, " + ", ".join(hs) + ") {",
+                    "  const int t = threadIdx.x;",
+                    f"  const int p0 = blockIdx.x * {rb}, p1 = min(ek_nwg, p0 + {rb});"]
+            for k, info in enumerate(self.priv.values()):
+                B, O, T_ = info["bins"], info["off"], total_words
+                t = ctype(info["dt"])
+                out += [f"  for (int b = 4 * t; b < {B}; b += 1024) {{",
+                        "    ek::i32x4 s = {0, 0, 0, 0};",
+                        "    #pragma unroll 8",
+                        f"    for (int w = p0; w < p1; ++w) s += __builtin_nontemporal_load("
+                        f"reinterpret_cast<const ek::i32x4*>(ek_part + (size_t)w * {T_} + {O} + b));",
+                        "    #pragma unroll",
+                        f"    for (int j = 0; j < 4; ++j) if (b + j < {B} && s[j]) "
+                        f"__hip_atomic_fetch_add(ek_h{k} + b + j, ({t})s[j], __ATOMIC_RELAXED, "
+                        "__HIP_MEMORY_SCOPE_AGENT);",
+                        "  }"]
+            out.append("}")
+            bases = [fn.args.index(i["base"]) for i in self.priv.values()]
+            flush = {"name": fname, "rb": rb, "bases": bases, "total": total_words}
         gk = GeneratedKernel(kname, "\n".join(out) + "\n", args, self.nw, self.lds, self.nt)
         gk.coarsen = int(self.coarsen)
         gk.asserts = list(self.asserts)
+        gk.flush = flush
         return gk
 
 
@@ -3066,6 +3119,21 @@ PID_REMAP = [
 
 def generate(fn: ir.Func, options: dict | None = None) -> GeneratedKernel:
     return Emitter(fn, options).run()
+
+
+def arg_offsets(kargs: list[KernelArg]) -> list[int]:
+    """Byte offset of each argument in the kernarg layout that `pack_args` builds."""
+    offs, n = [], 0
+    for ka in kargs:
+        if ka.kind == "ptr":
+            size = 8
+        else:
+            size = {"int32_t": 4, "int64_t": 8, "uint32_t": 4, "uint64_t": 8, "float": 4,
+                    "int16_t": 2, "uint16_t": 2, "int8_t": 1, "uint8_t": 1}[ka.cparam]
+        n += (-n) % size
+        offs.append(n)
+        n += size
+    return offs
 
 
 def pack_args(kargs: list[KernelArg], values: list, pad8: bool = True) -> bytes:

@@ -129,9 +129,67 @@ class CompiledKernel:
         return self._attrs
 
     def pack(self, values) -> bytes:
+        values = list(values)
+        if self.gen.flush:
+            values.append(0)      # the partial-bin buffer, set per stream at launch
         b = codegen_hip.pack_args(self.args, values, pad8=not self.gen.coarsen)
         self.packed_size = len(b)
         return b
+
+    def _flush_function(self):
+        if getattr(self, "_flush_fn", None) is None:
+            self.function()
+            f = ctypes.c_void_p()
+            hip.call("ek_module_function", self._module, self.gen.flush["name"].encode(),
+                     ctypes.byref(f))
+            self._flush_fn = f
+        return self._flush_fn
+
+    def _partials(self, stream: int, nwg: int) -> int:
+        """The partial-bin buffer for launches on `stream` (kept for the kernel's life;
+        launches of one specialization on one stream run in order, so they can share it)."""
+        bufs = self.__dict__.setdefault("_part_bufs", {})
+        need = max(16, nwg * self.gen.flush["total"] * 4)
+        cur = bufs.get(stream)
+        if cur is None or cur[1] < need:
+            from enceladus_amd.runtime import tensor as T
+            from enceladus_amd.language import core as _core
+            t = T.Tensor((need,), _core.uint8)
+            bufs[stream] = (t, need)
+            cur = bufs[stream]
+        return cur[0].ptr
+
+    def prepare(self, grid, kernarg: bytes, stream: int = 0) -> list:
+        """The dispatches of one logical launch: [(function, (gx, gy, gz), block, kernarg
+        buffer, size)]: the kernel itself, then the second flush level when it has one."""
+        gx, gy, gz = (tuple(grid) + (1, 1, 1))[:3]
+        if gx == 0 or gy == 0 or gz == 0:
+            return []
+        (gx, gy, gz), extra = self.launch_grid(grid)
+        if extra:
+            kernarg = kernarg[:self.packed_size] + extra
+            kernarg += b"\0" * ((-len(kernarg)) % 8)
+        out = []
+        fl = self.gen.flush
+        if fl:
+            import struct
+            offs = codegen_hip.arg_offsets(self.args)
+            part = self._partials(stream, gx)
+            kb = bytearray(kernarg)
+            struct.pack_into("<Q", kb, offs[-1], part)
+            kernarg = bytes(kb)
+            bases = [struct.unpack_from("<Q", kernarg, offs[i])[0] for i in fl["bases"]]
+            fargs = [codegen_hip.KernelArg("p", "ptr", None, "int32_t*"),
+                     codegen_hip.KernelArg("n", "scalar", None, "int32_t")] + \
+                [codegen_hip.KernelArg("h", "ptr", None, "int32_t*") for _ in bases]
+            fk = codegen_hip.pack_args(fargs, [part, gx, *bases])
+        buf = ctypes.create_string_buffer(kernarg, len(kernarg))
+        out.append((self.function(), (gx, gy, gz), self.gen.block, buf, len(kernarg)))
+        if fl:
+            fbuf = ctypes.create_string_buffer(fk, len(fk))
+            out.append((self._flush_function(), ((gx + fl["rb"] - 1) // fl["rb"], 1, 1), 256,
+                        fbuf, len(fk)))
+        return out
 
     def launch_grid(self, grid):
         """(launch grid, extra kernarg bytes) for a logical program grid."""
@@ -144,21 +202,15 @@ class CompiledKernel:
         return (min(total, cap), 1, 1), struct.pack("<iii", gx, gy, gz)
 
     def launch_raw(self, grid, kernarg: bytes, stream: int = 0):
-        gx, gy, gz = (tuple(grid) + (1, 1, 1))[:3]
-        if gx == 0 or gy == 0 or gz == 0:
-            return
-        (gx, gy, gz), extra = self.launch_grid(grid)
-        if extra:
-            kernarg = kernarg[:self.packed_size] + extra
-            kernarg += b"\0" * ((-len(kernarg)) % 8)
-        buf = ctypes.create_string_buffer(kernarg, len(kernarg))
         from enceladus_amd.runtime import debug
-        t0 = debug.before_launch(stream) if debug._active is not None else None
-        hip.call("ek_launch", ctypes.c_void_p(stream or None), self.function(), gx, gy, gz,
-                 self.gen.block, 1, 1, 0, buf, len(kernarg))
-        if t0 is not None:
-            debug.after_launch(t0, stream, self.name, (gx, gy, gz), self.gen.block,
-                               self.gen.lds_bytes)
+        for fn_, g_, blk, buf, n in self.prepare(grid, kernarg, stream):
+            t0 = debug.before_launch(stream) if debug._active is not None else None
+            hip.call("ek_launch", ctypes.c_void_p(stream or None), fn_, g_[0], g_[1], g_[2],
+                     blk, 1, 1, 0, buf, n)
+            if t0 is not None:
+                nm = self.name if fn_ is self._function else self.gen.flush["name"]
+                debug.after_launch(t0, stream, nm, g_, blk,
+                                   self.gen.lds_bytes if fn_ is self._function else 0)
 
 
 _CAP = None

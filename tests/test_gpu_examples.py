@@ -101,10 +101,14 @@ def test_cumsum_int32(shape, reverse):
     assert np.array_equal(got, R.cumsum(x, reverse))
 
 
-@pytest.mark.parametrize("n,bins", [(1 << 20, 1024), (100_003, 64), (5000, 4096)])
-def test_histogram(n, bins):
+@pytest.mark.parametrize("n,bins", [(1 << 20, 1024), (100_003, 64), (5000, 4096),
+                                    (70_001, 100), (70_001, 6)])
+@pytest.mark.parametrize("flush", ["two_level", "atomic"])
+def test_histogram(n, bins, flush, monkeypatch):
     from examples.histogram import histogram
-    _say(f"histogram n={n} bins={bins}")
+    _say(f"histogram n={n} bins={bins} flush={flush}")
+    if flush == "atomic":
+        monkeypatch.setenv("ENCELADUS_CODEGEN", "priv_flush=atomic")
     x = np.random.default_rng(0).integers(0, bins, n, dtype=np.int32)
     got = histogram(x, bins, 0.0, float(bins))
     assert np.array_equal(got, R.histogram(x, bins, 0.0, float(bins)))
