@@ -981,6 +981,24 @@ class Emitter:
             return
         lay = self.lay[res.id]
         nm = self.fresh("t")
+        rs = self._rescale(res, lay)
+        if rs is not None:
+            # acc * scale[:, None]: a wave whose factors are all exactly 1 skips the multiply
+            # (x * 1 == x), the common case in online softmax once the row maxima settle
+            ea, es = self.elem(rs[0], lay, "r"), self.elem(rs[1], lay, "r")
+            self.emit(f"float {nm}[{lay.nregs}];")
+            self.emit("{")
+            self.emit("  bool ek_any = false;")
+            self.emit("  #pragma unroll")
+            self.emit(f"  for (int r = 0; r < {lay.nregs}; ++r) {{ {nm}[r] = {ea}; "
+                      f"ek_any |= ({es} != 1.0f); }}")
+            self.emit("  if (__builtin_amdgcn_ballot_w64(ek_any) != 0) {")
+            self.emit("    #pragma unroll")
+            self.emit(f"    for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] *= {es};")
+            self.emit("  }")
+            self.emit("}")
+            self.define(res, nm)
+            return
         xs = [self.elem(o, lay, "r") if self.tile(o) else self.name[o.id] for o in op.operands]
         cond = None
         if op.name == "select" and self.tile(op.operands[0]) and \
@@ -2003,6 +2021,25 @@ class Emitter:
         self.emit(f"    #pragma unroll")
         self.emit(f"    for (int j = 0; j < {n}; j += {V}) ek::vload<{T}, {V}>(&{dst}[j], "
                   f"&{sm}[{idx}]);")
+
+    def _rescale(self, c: ir.Value, lc):
+        """(acc, scale) when `c` is `acc * scale` in fp32, with `acc` a register tile in
+        layout `lc` (an accumulator) and `scale` a broadcast of a lower-rank tile (one
+        factor per row, as in the online-softmax rescale); None otherwise."""
+        if self.opt.get("no_rescale_skip") or c.op is None or c.op.name != "binary" or \
+                c.op.attrs.get("op") != "mul" or c.type.dtype is not core.float32 or \
+                lc.nregs < 16:
+            return None
+        for a, b in (c.op.operands, c.op.operands[::-1]):
+            if self.kind.get(a.id) != "anchored" or self.lay[a.id].key() != lc.key():
+                continue
+            x = b
+            while x.op is not None and x.op.name in ("broadcast", "expand_dims"):
+                x = x.op.operands[0]
+            if x is not b and len(x.type.shape) < len(c.type.shape) and x.type.numel <= \
+                    c.type.shape[0]:
+                return a, b
+        return None
 
     def op_dot_int(self, op):
         """A product without MFMA: integer operands other than int8 (uint8, 16- and 32-bit),
