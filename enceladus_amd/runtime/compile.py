@@ -25,7 +25,7 @@ import sys
 import threading
 from pathlib import Path
 
-from enceladus_amd.compiler import codegen_hip, frontend, ir, widen
+from enceladus_amd.compiler import codegen_hip, frontend, ir, rewrite, widen
 from enceladus_amd.runtime import hip
 
 log = logging.getLogger("enceladus")
@@ -252,5 +252,7 @@ def build_module(jfn, arg_types, arg_facts, constexprs, num_warps, options) -> i
     fn = frontend.build_ir(jfn.fn, arg_types, arg_facts, constexprs, num_warps, options)
     if widen.needs_idx64(fn):
         widen.widen_index_math(fn)
+    if not (options or {}).get("no_scale_fold"):
+        rewrite.fold_softmax_scale(fn)
     ir.dce(fn)
     return fn

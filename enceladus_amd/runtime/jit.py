@@ -74,8 +74,11 @@ def _data_ptr(value: Any) -> int | None:
 
 
 def arg_facts(value: Any) -> dict:
-    if isinstance(value, (bool, np.bool_, float, np.floating)):
+    if isinstance(value, (bool, np.bool_)):
         return {}
+    if isinstance(value, (float, np.floating)):
+        # the sign of a float (an attention scale) lets the compiler fold it through max
+        return {"positive": True} if float(value) > 0 else {}
     if isinstance(value, (int, np.integer)):
         v = int(value)
         f = {}

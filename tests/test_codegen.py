@@ -299,3 +299,26 @@ def test_idx64_fact_from_element_span():
         def stride(self):
             return (1 << 31, 1)
     assert jit._last_index(_Strided()) == (1 << 31) + (1 << 30) - 1 > jit.MAX_ELEMENT_INDEX
+
+
+def test_softmax_scale_fold():
+    """With a positive scale the attention loop reduces raw scores and scales only the row
+    maxima (max commutes with a positive scale exactly); a negative scale keeps the
+    per-score multiply (reference kernel: examples/08_flash_attention.py:30-127)."""
+    import torch
+    from examples.flash_attention import attention_kernel
+    bf = torch.zeros(16, dtype=torch.bfloat16)
+
+    def ops(scale):
+        f = attention_kernel.ir_for(bf, bf, bf, bf, scale, 256, 256 * 64, 64, HEAD_DIM=64,
+                                    BLOCK_M=64, BLOCK_N=32, CAUSAL=True, dot_warps=(4, 1))
+        return [op for op in ir.walk(f.body)]
+    pos = ops(0.125)
+    assert any(op.name == "fma" for op in pos)
+    red = [op for op in pos if op.name == "reduce" and op.attrs["kind"] == "max"][0]
+    src = red.operands[0].op
+    assert src.name == "select" and src.operands[1].op.name == "dot"
+    neg = ops(-0.125)
+    assert not any(op.name == "fma" for op in neg)
+    red = [op for op in neg if op.name == "reduce" and op.attrs["kind"] == "max"][0]
+    assert red.operands[0].op.operands[1].op.name == "binary"

@@ -190,6 +190,20 @@ def test_flash_attention_fp16(causal, n, d, bm, bn):
     np.testing.assert_allclose(got, want, rtol=2e-3, atol=2e-3)
 
 
+@pytest.mark.parametrize("scale", [-0.07, 0.3])
+def test_flash_attention_scale_sign(scale):
+    """A negative scale compiles the kernel without the max/scale fold (the launch's
+    `positive` fact is absent); both signs match the float64 reference."""
+    from examples.flash_attention import attention
+    _say(f"flash attention fp16 scale={scale}")
+    rng = np.random.default_rng(1)
+    q, k, v = (rng.standard_normal((1, 2, 256, 64), dtype=np.float32).astype(np.float16)
+               for _ in range(3))
+    got = attention(q, k, v, True, sm_scale=scale, block_m=64, block_n=32).astype(np.float64)
+    want = R.attention(q, k, v, True, sm_scale=scale)
+    np.testing.assert_allclose(got, want, rtol=2e-3, atol=2e-3)
+
+
 @pytest.mark.parametrize("m,n,k,bm,bn,bk,nw", [(512, 512, 256, 256, 256, 64, 4),
                                                 (256, 512, 128, 128, 256, 32, 4),
                                                 (512, 256, 192, 256, 128, 64, 4),
