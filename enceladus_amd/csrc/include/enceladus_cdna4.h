@@ -750,6 +750,7 @@ struct GemmDma {
     }
   }
 
+  template <int KK0, int KK1>
   EK_INLINE void compute(float* acc, const uint16_t* st, int lane, int wm, int wn) {
     typedef short v4s __attribute__((ext_vector_type(4)));
     const u32x4* sA = reinterpret_cast<const u32x4*>(st);
@@ -757,7 +758,7 @@ struct GemmDma {
     const int r32 = lane & 31, h = lane >> 5;
     const int g = lane >> 4, ti = (lane >> 2) & 3, tq = lane & 3;
 #pragma unroll
-    for (int kk = 0; kk < TK; ++kk) {
+    for (int kk = KK0; kk < KK1; ++kk) {
       T a[TM][8], b[TN][8];
       const int kc = kk * 2 + h;
 #pragma unroll
@@ -807,8 +808,11 @@ struct GemmDma {
       // this wave's copies of stage `it` have landed (S - 2 younger stages may still fly),
       // its reads of the previous stage are complete; then everyone's are.
       asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((S - 2) * D) : "memory");
+      // the first k slice's fragment reads go out before the copies, so their latency
+      // hides behind the copy issue instead of stalling the first MFMA
+      compute<0, 1>(acc, s16 + (it % S) * STAGE, lane, wm, wn);
       copy(ra, rb, ldb, K, lo + (it + S - 1) * BK, l0 + ((it + S - 1) % S) * STAGE * 2, wave);
-      compute(acc, s16 + (it % S) * STAGE, lane, wm, wn);
+      compute<1, TK>(acc, s16 + (it % S) * STAGE, lane, wm, wn);
     }
     // drain the copies issued past the end before anyone reuses the LDS
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
