@@ -2742,7 +2742,8 @@ class Emitter:
             d = (bm * bk // 8 + bk * bn // 8) // self.nt
             while nst > 2 and ((nst - 2) * d > 63 or nst * stage > 163840):
                 nst -= 1
-            tmpl = f"ek::GemmDma<{T}, {bm}, {bn}, {bk}, {p.wm}, {p.wn}, {self.nt}, {nst}>"
+            split = min(bk // 16, int(self.opt.get("gemm_split", 1)))
+            tmpl = f"ek::GemmDma<{T}, {bm}, {bn}, {bk}, {p.wm}, {p.wn}, {self.nt}, {nst}, {split}>"
             self.need_lds(nst * stage)
         else:
             tmpl = (f"ek::Gemm<{T}, {bm}, {bn}, {bk}, {p.wm}, {p.wn}, {self.nt}, "

@@ -691,7 +691,7 @@ struct Gemm {
 //    k * NCB + (nc ^ (((k >> RSH) & RMASK) << 2)), which spreads the 4 rows a transpose
 //    read touches over the 4 64-byte quarters of a pass.
 // ---------------------------------------------------------------------------
-template <typename T, int BM, int BN, int BK, int WM, int WN, int NT, int S>
+template <typename T, int BM, int BN, int BK, int WM, int WN, int NT, int S, int SPLIT = 1>
 struct GemmDma {
   static constexpr int TM = BM / WM / 32, TN = BN / WN / 32, TK = BK / 16;
   static constexpr int KC = BK / 8;                       // A chunks per row
@@ -711,6 +711,7 @@ struct GemmDma {
   static_assert(WM * WN * 64 == NT, "warps must tile the block");
   static_assert(S >= 2 && (S - 2) * D <= 63, "vmcnt range");
   static_assert(NCB >= 4 * (RMASK + 1), "B swizzle needs the row's chunks");
+  static_assert(SPLIT >= 0 && SPLIT <= TK, "copies issue after SPLIT of the TK k slices");
 
   static EK_INLINE int a_chunk(int row, int kc) { return row * KC + (kc ^ ((row >> ASH) & AMASK)); }
   static EK_INLINE int b_chunk(int k, int nc) { return k * NCB + (nc ^ (((k >> RSH) & RMASK) << 2)); }
@@ -738,10 +739,16 @@ struct GemmDma {
 
   // Copies the k-th tile (k = first column of A / row of B) into the stage at LDS byte `st`.
   EK_INLINE void copy(i32x4 ra, i32x4 rb, int ldb, int K, int k, uint32_t st, int wave) {
+    if (k + BK <= K) {
+      // the whole k slice lies inside A: no per-chunk column test
 #pragma unroll
-    for (int i = 0; i < A_DMA; ++i) {
-      const int off = (k + a_kc[i] + 8 <= K) ? (a_off[i] + k) * 2 : kOOB;
-      dma16(ra, st + (i * NT + wave * 64) * 16, off);
+      for (int i = 0; i < A_DMA; ++i) dma16(ra, st + (i * NT + wave * 64) * 16, (a_off[i] + k) * 2);
+    } else {
+#pragma unroll
+      for (int i = 0; i < A_DMA; ++i) {
+        const int off = (k + a_kc[i] + 8 <= K) ? (a_off[i] + k) * 2 : kOOB;
+        dma16(ra, st + (i * NT + wave * 64) * 16, off);
+      }
     }
 #pragma unroll
     for (int i = 0; i < B_DMA; ++i) {
@@ -810,9 +817,9 @@ struct GemmDma {
       asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((S - 2) * D) : "memory");
       // the first k slice's fragment reads go out before the copies, so their latency
       // hides behind the copy issue instead of stalling the first MFMA
-      compute<0, 1>(acc, s16 + (it % S) * STAGE, lane, wm, wn);
+      compute<0, SPLIT>(acc, s16 + (it % S) * STAGE, lane, wm, wn);
       copy(ra, rb, ldb, K, lo + (it + S - 1) * BK, l0 + ((it + S - 1) % S) * STAGE * 2, wave);
-      compute<1, TK>(acc, s16 + (it % S) * STAGE, lane, wm, wn);
+      compute<SPLIT, TK>(acc, s16 + (it % S) * STAGE, lane, wm, wn);
     }
     // drain the copies issued past the end before anyone reuses the LDS
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");

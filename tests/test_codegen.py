@@ -116,7 +116,7 @@ def test_descriptor_dot_loop_uses_gemm_template():
     src = codegen_hip.generate(matmul_desc_kernel.ir_for(
         f16, f16, f16, 4096, 4096, 4096, 4096, 4096, 4096, BM=256, BN=256, BK=64)).source
     # aligned operands within 2 GiB: the LDS-DMA pipeline (64 KB stages, 2 of them)
-    assert "ek::GemmDma<_Float16, 256, 256, 64, 2, 2, 256, 2>" in src
+    assert "ek::GemmDma<_Float16, 256, 256, 64, 2, 2, 256, 2, 1>" in src
     # K and N not known to be multiples of 8: the template reads the row tails elementwise
     src3 = codegen_hip.generate(matmul_desc_kernel.ir_for(
         f16, f16, f16, 256, 250, 100, 112, 256, 250, BM=128, BN=128, BK=64)).source
