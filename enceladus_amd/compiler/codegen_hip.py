@@ -2162,6 +2162,14 @@ class Emitter:
         self.emit("    #pragma unroll")
         self.emit(f"    for (int in_ = 0; in_ < {tn}; ++in_) "
                   f"ek::{ins.fn}(&{nm}[(im * {tn} + in_) * {nacc}], {x}, {y});")
+        dd = getattr(self, "deferred_dma", None)
+        if (sa or sb) and dd is not None and not dd["used"] and tk > 1:
+            # the loop's stage copies, after this dot's first k slice
+            dd["used"] = True
+            self.emit("  if (kk == 0) {")
+            for ln in dd["lines"]:
+                self.emit("    " + ln)
+            self.emit("  }")
         self.emit("}")
         if cdt not in (core.float32, core.int32):
             out = self.fresh("acch")
@@ -2837,10 +2845,20 @@ class Emitter:
             # everyone's are, so the previous stage can be refilled.
             self.emit(f'asm volatile("s_waitcnt vmcnt({(nst - 2) * dcount}) lgkmcnt(0)\\n\\t'
                       f's_barrier" ::: "memory");')
+            lines = []
             for info in stg:
-                for ln in self._stage_dma(info, f"({ivn} + {nst - 1} * {step})",
-                                          f"(ek_it{li} + {nst - 1}) % {nst}"):
-                    self.emit(ln)
+                lines += self._stage_dma(info, f"({ivn} + {nst - 1} * {step})",
+                                         f"(ek_it{li} + {nst - 1}) % {nst}")
+            # The copies for a later stage may go anywhere after the barrier: the first dot
+            # that reads a stage issues them after its first k slice (its fragment reads go
+            # out first and hide behind the copy issue); otherwise they land here.
+            slot: list = []
+            self.cur.items.append(slot)
+            prev_dma = getattr(self, "deferred_dma", None)
+            self.deferred_dma = None if self.opt.get("no_late_dma") else \
+                {"lines": lines, "used": False}
+            if self.deferred_dma is None:
+                slot.extend(self.cur.indent + ln for ln in lines)
         elif stg:
             self.in_staged_loop = getattr(self, "in_staged_loop", 0) + 1
             self.emit(f"const bool ek_more{li} = {ivn} + {step} < {hi};")
@@ -2851,6 +2869,10 @@ class Emitter:
             self.emit("}")
         self.gen_block(body)
         if dma:
+            d = self.deferred_dma
+            if d is not None and not d["used"]:
+                slot.extend(self.cur.indent + ln for ln in d["lines"])
+            self.deferred_dma = prev_dma
             self.emit(f"++ek_it{li};")
             self.in_staged_loop -= 1
         elif stg:
