@@ -1919,7 +1919,15 @@ class Emitter:
             self.emit(f"for (int o = 0; o < {outer}; ++o) {{ {nm}_t[o] = {nm}_x[o * {run} + "
                       f"{last}]; {nm}_p[o] = {nm}_t[o]; }}")
             low = 0
-            for i in lane_bits:
+            dpp = (lane_bits == list(range(6)) and not rev and acc_t in ("int32_t", "uint32_t",
+                                                                         "float") and
+                   not self.opt.get("no_dpp_scan"))
+            if dpp:
+                # all 64 lanes walk the axis in order: one DPP prefix sum per run
+                self.emit("#pragma unroll")
+                self.emit(f"for (int o = 0; o < {outer}; ++o) {nm}_p[o] = "
+                          f"ek::wave_prefix_sum<{acc_t}>({nm}_p[o]);")
+            for i in ([] if dpp else lane_bits):
                 bit = 1 << i
                 if not rev:
                     srcl = f"((ek_lane & ~{bit}) | {low})"

@@ -253,6 +253,28 @@ template <int MASK, typename T> EK_INLINE T shfl_xor(T v) {
   }
 }
 
+// Inclusive prefix sum over lanes 0..63 of a 32-bit value with DPP moves: Kogge-Stone
+// inside each 16-lane row (row_shr 1, 2, 4, 8), then row_bcast:15 carries row 0 into
+// row 1 and row 2 into row 3, and row_bcast:31 carries lane 31 into rows 2 and 3. Lanes
+// whose DPP source is out of range (or outside the row mask) add 0.
+template <typename T> EK_INLINE T wave_prefix_sum(T v) {
+  static_assert(sizeof(T) == 4, "32-bit values");
+  int x = __builtin_bit_cast(int, v);
+#define EK_SCAN_STEP(ctrl, rmask)                                                        \
+  {                                                                                     \
+    const int y = __builtin_amdgcn_update_dpp(0, x, ctrl, rmask, 0xF, false);           \
+    x = __builtin_bit_cast(int, __builtin_bit_cast(T, x) + __builtin_bit_cast(T, y));  \
+  }
+  EK_SCAN_STEP(0x111, 0xF)   // row_shr:1
+  EK_SCAN_STEP(0x112, 0xF)   // row_shr:2
+  EK_SCAN_STEP(0x114, 0xF)   // row_shr:4
+  EK_SCAN_STEP(0x118, 0xF)   // row_shr:8
+  EK_SCAN_STEP(0x142, 0xA)   // row_bcast:15 into rows 1 and 3
+  EK_SCAN_STEP(0x143, 0xC)   // row_bcast:31 into rows 2 and 3
+#undef EK_SCAN_STEP
+  return __builtin_bit_cast(T, x);
+}
+
 // ---------------------------------------------------------------------------
 // Combine functions for reductions and scans.
 // ---------------------------------------------------------------------------
