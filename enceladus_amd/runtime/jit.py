@@ -179,6 +179,10 @@ class Launcher:
         packed = []
         for i, v in enumerate(values):
             if T.is_array_like(v):
+                if i in self.writes and isinstance(v, np.ndarray) and not v.flags.writeable:
+                    raise ValueError(
+                        f"argument `{self.runtime_names[i]}` is a read-only NumPy array, and "
+                        "the kernel writes it; pass a writable array (for example a copy)")
                 b = T.bind_array(v)
                 b.writeback = i in self.writes
                 bindings.append(b)

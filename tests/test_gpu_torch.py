@@ -183,3 +183,19 @@ def test_capture_writes_a_dispatch_trace(tmp_path):
     assert all(e["dur"] > 0 and e["args"]["grid"][0] == 1024 for e in ev)
     assert ev[0]["ts"] <= ev[1]["ts"] <= ev[2]["ts"]
     torch.testing.assert_close(out, 2 * x)
+
+
+def test_writes_to_read_only_numpy_arrays_are_refused():
+    """A kernel may read a read-only array but must not write one (reference:
+    tests/test_runtime.py:333-355)."""
+    from examples.vector_add import add_kernel
+    print("[case] read-only numpy", flush=True)
+    ro = np.frombuffer(bytes(32), np.float32)
+    host = np.zeros(8, np.float32)
+    add_kernel[(1,)](ro, ro, host, 8, BLOCK=8)
+    np.testing.assert_array_equal(host, 0.0)
+    with pytest.raises(ValueError, match="read-only NumPy array"):
+        add_kernel[(1,)](host, host, ro, 8, BLOCK=8)
+    with pytest.raises(ValueError, match="read-only NumPy array"):
+        add_kernel[(1,)](host, host, np.broadcast_to(np.zeros(1, np.float32), (8,)), 8, BLOCK=8)
+    assert not np.frombuffer(ro.tobytes(), np.float32).any()
