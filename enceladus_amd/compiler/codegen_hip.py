@@ -140,8 +140,9 @@ class GeneratedKernel:
     block: int
     coarsen: int = 0       # workgroups per CU of a coarsened launch (0: one per program)
     asserts: list = field(default_factory=list)   # tl.device_assert sites (message, loc)
-    # two-level histogram flush: {"name", "rb", "bases" (arg indices), "total" (words per
-    # workgroup row of the partial buffer)}; the launcher runs `name` after the kernel
+    # two-level histogram flush: {"name", "rb" (rows per flush workgroup), "bases" (arg
+    # indices), "total" (words per workgroup row of the partial buffer), "chunks" (64-word
+    # column chunks)}; the launcher runs `name` on grid (chunks, rows / rb) after the kernel
     flush: dict | None = None
 
 
@@ -3012,9 +3013,10 @@ class Emitter:
             params.append("uint32_t* ek_assert_buf")
             args.append(KernelArg("ek_assert_buf", "ptr", core.uint32, "uint32_t*"))
         # Two-level flush of privatised bins: each workgroup stores its bins to a partial
-        # buffer row (plain stores), and a second kernel sums RB rows at a time and adds each
-        # sum with one global atomic. Measured on the 1024-bin histogram: 71 -> 56 us; one
-        # global atomic per bin per workgroup (2,048 per address) cost about 29 us.
+        # buffer row (plain stores), and a second kernel sums a block of RB rows by 64 words
+        # and adds each sum with one global atomic. Measured on the 1024-bin histogram: one
+        # global atomic per bin per workgroup (2,048 per address) cost about 29 us; 32-row
+        # blocks across all bins (64 atomics per address) 7.6 us.
         two = bool(self.priv) and bool(self.coarsen) and self.priv_copies == 1 and \
             self.opt.get("priv_flush", "two_level") != "atomic" and \
             all(i["dt"].primitive_bitwidth == 32 for i in self.priv.values())
@@ -3131,32 +3133,46 @@ class Emitter:
         out.append("}")
         flush = None
         if two:
-            rb = int(self.opt.get("priv_flush_rows", 32))
+            rb = int(self.opt.get("priv_flush_rows", 256))
             fname = f"{kname}_flush"
-            hs = [f"{ctype(i['dt'])}* ek_h{k}" for k, i in enumerate(self.priv.values())]
-            out += ["", "// Second level of the privatised-bin flush: workgroup x sums partial rows",
-                    f"// [x*{rb}, x*{rb}+{rb}) with 16-byte loads and adds each non-zero sum to the "
-                    "kernel's bins.",
+            T_ = total_words
+            infos = list(self.priv.values())
+            hs = [f"{ctype(i['dt'])}* ek_h{k}" for k, i in enumerate(infos)]
+            out += ["", "// Second level of the privatised-bin flush: workgroup (x, y) sums words "
+                    f"[64x, 64x+64) of the partial", f"// rows [y*{rb}, y*{rb}+{rb}), 16 rows at a "
+                    "time with 16-byte loads, reduces the 16 row lanes in LDS",
+                    "// and adds each non-zero sum to the kernel's bins with one atomic.",
                     f'extern "C" __global__ void __launch_bounds__(256) {fname}('
                     "const int32_t* __restrict__ ek_part, int32_t ek_nwg, " + ", ".join(hs) + ") {",
-                    "  const int t = threadIdx.x;",
-                    f"  const int p0 = blockIdx.x * {rb}, p1 = min(ek_nwg, p0 + {rb});"]
-            for k, info in enumerate(self.priv.values()):
-                B, O, T_ = info["bins"], info["off"], total_words
-                t = ctype(info["dt"])
-                out += [f"  for (int b = 4 * t; b < {B}; b += 1024) {{",
-                        "    ek::i32x4 s = {0, 0, 0, 0};",
-                        "    #pragma unroll 8",
-                        f"    for (int w = p0; w < p1; ++w) s += __builtin_nontemporal_load("
-                        f"reinterpret_cast<const ek::i32x4*>(ek_part + (size_t)w * {T_} + {O} + b));",
-                        "    #pragma unroll",
-                        f"    for (int j = 0; j < 4; ++j) if (b + j < {B} && s[j]) "
-                        f"__hip_atomic_fetch_add(ek_h{k} + b + j, ({t})s[j], __ATOMIC_RELAXED, "
-                        "__HIP_MEMORY_SCOPE_AGENT);",
-                        "  }"]
-            out.append("}")
-            bases = [fn.args.index(i["base"]) for i in self.priv.values()]
-            flush = {"name": fname, "rb": rb, "bases": bases, "total": total_words}
+                    "  __shared__ int32_t ek_red[16][64];",
+                    "  const int t = threadIdx.x, seg = t & 15, rl = t >> 4;",
+                    "  const int w0 = blockIdx.x * 64 + seg * 4;",
+                    f"  const int p0 = blockIdx.y * {rb}, p1 = min(ek_nwg, p0 + {rb});",
+                    "  ek::i32x4 s = {0, 0, 0, 0};",
+                    f"  if (w0 < {T_}) {{",
+                    "    #pragma unroll 8",
+                    "    for (int w = p0 + rl; w < p1; w += 16) s += __builtin_nontemporal_load("
+                    f"reinterpret_cast<const ek::i32x4*>(ek_part + (size_t)w * {T_} + w0));",
+                    "  }",
+                    "  #pragma unroll",
+                    "  for (int j = 0; j < 4; ++j) ek_red[rl][seg * 4 + j] = s[j];",
+                    "  __syncthreads();",
+                    "  if (t < 64) {",
+                    "    int32_t v = 0;",
+                    "    #pragma unroll",
+                    "    for (int r = 0; r < 16; ++r) v += ek_red[r][t];",
+                    "    const int w = blockIdx.x * 64 + t;",
+                    "    if (v) {"]
+            for k, info in enumerate(infos):
+                B, O = info["bins"], info["off"]
+                kw = "if" if k == 0 else "else if"
+                out.append(f"      {kw} (w >= {O} && w < {O + B}) __hip_atomic_fetch_add("
+                           f"ek_h{k} + (w - {O}), ({ctype(info['dt'])})v, __ATOMIC_RELAXED, "
+                           "__HIP_MEMORY_SCOPE_AGENT);")
+            out += ["    }", "  }", "}"]
+            bases = [fn.args.index(i["base"]) for i in infos]
+            flush = {"name": fname, "rb": rb, "bases": bases, "total": total_words,
+                     "chunks": (total_words + 63) // 64}
         gk = GeneratedKernel(kname, "\n".join(out) + "\n", args, self.nw, self.lds, self.nt)
         gk.coarsen = int(self.coarsen)
         gk.asserts = list(self.asserts)

@@ -187,7 +187,7 @@ class CompiledKernel:
         out.append((self.function(), (gx, gy, gz), self.gen.block, buf, len(kernarg)))
         if fl:
             fbuf = ctypes.create_string_buffer(fk, len(fk))
-            out.append((self._flush_function(), ((gx + fl["rb"] - 1) // fl["rb"], 1, 1), 256,
+            out.append((self._flush_function(), (fl["chunks"], (gx + fl["rb"] - 1) // fl["rb"], 1), 256,
                         fbuf, len(fk)))
         return out
 
