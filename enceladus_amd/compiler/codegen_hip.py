@@ -1568,26 +1568,45 @@ class Emitter:
 
     # -- atomics --------------------------------------------------------------------
     def _atomic_call(self, kind: str, t: str, dt: core.dtype, p: str, v: str, cmp=None) -> str:
+        """One atomic on element pointer `p`, returning the old value (reference:
+        codegen/atomic.py:44-135). 32-bit integer and float add, 32/64-bit integer
+        max/min, 32-bit bitwise ops, exchange and integer compare-and-swap are native;
+        float max/min (NaN-ignoring, as fmax/fmin), float compare-and-swap (a value compare,
+        so -0.0 matches 0.0) and every 8/16-bit element go through `ek::atomic_update`."""
         scope = "__ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT"
+        sub = dt.primitive_bitwidth < 32
+        fl = dt.is_floating()
+        if not sub:
+            if kind == "add":
+                return f"__hip_atomic_fetch_add({p}, {v}, {scope})"
+            if kind in ("and", "or", "xor"):
+                return f"__hip_atomic_fetch_{kind}({p}, {v}, {scope})"
+            if kind == "xchg":
+                return f"__hip_atomic_exchange({p}, {v}, {scope})"
+            if kind in ("max", "min") and not fl:
+                return f"__hip_atomic_fetch_{kind}({p}, {v}, {scope})"
+            if kind == "cas" and not fl:
+                return (f"([&]() {{ {t} o = {cmp}; __hip_atomic_compare_exchange_strong({p}, "
+                        f"&o, {v}, __ATOMIC_RELAXED, __ATOMIC_RELAXED, "
+                        "__HIP_MEMORY_SCOPE_AGENT); return o; })()")
+        f32 = (lambda x: f"ek::f32_or_self({x})") if fl else (lambda x: x)
         if kind == "add":
-            return f"__hip_atomic_fetch_add({p}, {v}, {scope})"
-        if kind in ("and", "or", "xor"):
-            return f"__hip_atomic_fetch_{kind}({p}, {v}, {scope})"
-        if kind == "xchg":
-            return f"__hip_atomic_exchange({p}, {v}, {scope})"
-        if kind in ("max", "min") and not dt.is_floating():
-            return f"__hip_atomic_fetch_{kind}({p}, {v}, {scope})"
-        if kind in ("max", "min"):
-            fnm = "__builtin_fmaxf" if kind == "max" else "__builtin_fminf"
-            return (f"([&]() {{ {t} o = __hip_atomic_load({p}, {scope}); "
-                    f"while (true) {{ {t} n = {fnm}(o, {v}); "
-                    f"if (__hip_atomic_compare_exchange_strong({p}, &o, n, __ATOMIC_RELAXED, "
-                    f"__ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break; }} return o; }})()")
-        if kind == "cas":
-            return (f"([&]() {{ {t} o = {cmp}; __hip_atomic_compare_exchange_strong({p}, &o, "
-                    f"{v}, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); "
-                    f"return o; }})()")
-        raise CompilationError(f"unknown atomic {kind}")
+            new = f"({t})(o + {v})"
+        elif kind in ("and", "or", "xor"):
+            new = f"({t})(o {_INFIX[kind]} {v})"
+        elif kind == "xchg":
+            new = f"({t})({v})"
+        elif kind in ("max", "min") and fl:
+            fn = "__builtin_fmaxf" if kind == "max" else "__builtin_fminf"
+            new = f"ek::Cvt<{t}>::from({fn}({f32('o')}, {f32(v)}))"
+        elif kind in ("max", "min"):
+            cmpop = ">" if kind == "max" else "<"
+            new = f"(o {cmpop} {v} ? o : ({t})({v}))"
+        elif kind == "cas":
+            new = f"({f32('o')} == {f32(cmp)} ? ({t})({v}) : o)"
+        else:
+            raise CompilationError(f"unknown atomic {kind}")
+        return f"ek::atomic_update({p}, [&]({t} o) -> {t} {{ return {new}; }})"
 
     def op_atomic_rmw(self, op):
         self._atomic(op, op.attrs["op"])
@@ -1620,7 +1639,7 @@ class Emitter:
             self.emit(f"  {t}* sm = reinterpret_cast<{t}*>(ek_smem);")
             self.emit("  __syncthreads();")
             self.emit(f"  if (ek_tid == 0) sm[0] = ({m}) ? {self._atomic_call(kind, t, dt, p, v, c)}"
-                      f" : ({t})0;")
+                      f" : {t}{{}};")
             self.emit("  __syncthreads();")
             self.emit(f"  {nm} = sm[0];")
             self.emit("}")
@@ -1647,9 +1666,6 @@ class Emitter:
                       f"__ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);")
             self.define(res, "ek_unused")
             return
-        if used and own:
-            raise CompilationError("the result of a tl.atomic_* on a tile with replicated "
-                                   "elements isn't supported; use a larger tile or fewer warps")
         nm = self.fresh("at")
         p = self.elem(ptr, lay, "r")
         v = self.elem(val_v, lay, "r")
@@ -1664,10 +1680,28 @@ class Emitter:
         self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {{")
         call = self._atomic_call(kind, t, dt, p, v, c)
         if conds:
-            self.emit(f"  {nm}[r] = ({' && '.join(conds)}) ? {call} : ({t})0;")
+            self.emit(f"  {nm}[r] = ({' && '.join(conds)}) ? {call} : {t}{{}};")
         else:
             self.emit(f"  {nm}[r] = {call};")
         self.emit("}")
+        if used and own:
+            # Replicated elements: only the owner thread ran the atomic, so the old values
+            # go through LDS to every thread that holds a copy (reference:
+            # codegen/atomic.py:208-231).
+            es = dt.itemsize
+            order = tuple(reversed(range(len(lay.shape))))
+            strides, total = self.lds_addr(lay.shape, order, es)
+            self.need_lds(total * es)
+            ix = self.lds_index(lay, strides, "r")
+            self.emit("{")
+            self.emit(f"  {t}* sm = reinterpret_cast<{t}*>(ek_smem);")
+            self.emit("  __syncthreads();")
+            self.emit("  #pragma unroll")
+            self.emit(f"  for (int r = 0; r < {lay.nregs}; ++r) if ({own}) sm[{ix}] = {nm}[r];")
+            self.emit("  __syncthreads();")
+            self.emit("  #pragma unroll")
+            self.emit(f"  for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = sm[{ix}];")
+            self.emit("}")
         self.define(res, nm)
 
     # -- join / split (reference: language/ops.py:832-902, codegen/msl.py:693-747) --------

@@ -507,6 +507,45 @@ EK_INLINE void assert_fail(uint32_t* buf, int index, int px, int py, int pz) {
     __hip_atomic_store(buf + 4, (uint32_t)pz, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
+// Atomic read-modify-write as a compare-and-swap loop: `f(old)` gives the new value. Used for
+// the updates without a native instruction: float max/min, value-compare CAS on floats, and
+// every 8- and 16-bit element, which is updated inside its aligned 32-bit word (the CAS
+// retries when a neighbour in the same word changed). Returns the old value.
+template <int N> struct UBits;
+template <> struct UBits<1> { typedef uint8_t type; };
+template <> struct UBits<2> { typedef uint16_t type; };
+template <> struct UBits<4> { typedef uint32_t type; };
+template <typename T, typename F> EK_INLINE T atomic_update(T* p, F f) {
+  static_assert(sizeof(T) == 1 || sizeof(T) == 2 || sizeof(T) == 4, "8/16/32-bit elements");
+  if constexpr (sizeof(T) == 4) {
+    uint32_t* w = reinterpret_cast<uint32_t*>(p);
+    uint32_t o = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    while (true) {
+      const T ov = __builtin_bit_cast(T, o);
+      const uint32_t n = __builtin_bit_cast(uint32_t, (T)f(ov));
+      if (n == o || __hip_atomic_compare_exchange_strong(w, &o, n, __ATOMIC_RELAXED,
+                                                        __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT))
+        return ov;
+    }
+  } else {
+    typedef typename UBits<sizeof(T)>::type Bits;
+    const uint64_t a = reinterpret_cast<uint64_t>(p);
+    uint32_t* w = reinterpret_cast<uint32_t*>(a & ~(uint64_t)3);
+    const int sh = (int)(a & 3) * 8;
+    const uint32_t m = (uint32_t)(Bits)~(Bits)0 << sh;
+    uint32_t o = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    while (true) {
+      const T ov = __builtin_bit_cast(T, (Bits)(o >> sh));
+      const uint32_t n = (o & ~m) | ((uint32_t)__builtin_bit_cast(Bits, (T)f(ov)) << sh);
+      if (n == o || __hip_atomic_compare_exchange_strong(w, &o, n, __ATOMIC_RELAXED,
+                                                        __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT))
+        return ov;
+    }
+  }
+}
+
 // tl.device_print: 16-bit floats print through float; everything else as itself.
 template <typename T> EK_INLINE T f32_or_self(T x) { return x; }
 EK_INLINE float f32_or_self(_Float16 x) { return (float)x; }
