@@ -1502,6 +1502,15 @@ class Emitter:
         else:
             out.append(v)
 
+    def _pos_step(self, op: ir.Op) -> bool:
+        """Whether a `for` op's step is a compile-time positive constant (the loop then
+        counts up with `iv < hi`; any other step takes the trip-count form)."""
+        v = op.operands[2]
+        while v.op is not None and v.op.name == "cast":
+            v = v.op.operands[0]
+        c = self._const_of(v)
+        return isinstance(c, int) and not isinstance(c, bool) and c > 0
+
     def _const_of(self, v: ir.Value):
         while v.op is not None and v.op.name in ("splat", "broadcast", "expand_dims"):
             v = v.op.operands[0]
@@ -2236,7 +2245,7 @@ class Emitter:
         for op in block.ops:
             for r in op.regions:
                 self.plan_staging(r)
-            if op.name != "for" or self.opt.get("no_staging"):
+            if op.name != "for" or self.opt.get("no_staging") or not self._pos_step(op):
                 continue
             body = op.regions[0]
             iv = body.args[0]
@@ -2811,6 +2820,8 @@ class Emitter:
 
     # -- control flow -----------------------------------------------------------------
     def op_for(self, op):
+        if not self._pos_step(op):
+            return self._general_for(op)
         if not self.opt.get("no_gemm_template"):
             g = self._gemm_match(op)
             if g is not None and self._emit_gemm_loop(op, g):
@@ -2933,6 +2944,46 @@ class Emitter:
         if dma:
             # copies issued past the last iteration land before anyone reuses the LDS
             self.emit('asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\\n\\ts_barrier" ::: "memory");')
+        for r, nm in zip(op.results, names):
+            self.define(r, nm)
+
+    def _general_for(self, op):
+        """Python `range` with a runtime or negative step: the trip count is computed once
+        in 64-bit unsigned arithmetic (exact for any bounds of the loop type), so the loop
+        always ends; a zero step runs no iterations (Python raises instead)."""
+        body = op.regions[0]
+        iv, carried = body.args[0], body.args[1:]
+        lo, hi, step = (self.name[o.id] for o in op.operands[:3])
+        names = []
+        for a, i in zip(carried, op.operands[3:]):
+            t = ctype(a.type.dtype) + ("*" if a.type.ptr else "")
+            nm = self.fresh("c")
+            names.append(nm)
+            if not self.tile(a):
+                self.emit(f"{t} {nm} = {self.name[i.id]};")
+            else:
+                lay = self.lay[a.id]
+                self.emit(f"{t} {nm}[{lay.nregs}];")
+                self.emit("#pragma unroll")
+                self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) {nm}[r] = "
+                          f"{self.elem(i, lay, 'r')};")
+        it = ctype(iv.type.dtype)
+        k = self.fresh("gl")
+        self.emit(f"const int64_t {k}_lo = (int64_t)({lo}), {k}_hi = (int64_t)({hi}), "
+                  f"{k}_st = (int64_t)({step});")
+        self.emit(f"const uint64_t {k}_n = {k}_st > 0 ? ({k}_hi > {k}_lo ? ((uint64_t){k}_hi - "
+                  f"(uint64_t){k}_lo - 1) / (uint64_t){k}_st + 1 : 0) : {k}_st < 0 ? ({k}_lo > "
+                  f"{k}_hi ? ((uint64_t){k}_lo - (uint64_t){k}_hi - 1) / (0 - (uint64_t){k}_st) "
+                  "+ 1 : 0) : 0;")
+        ivn = self.fresh("iv")
+        self.push_scope(f"for (uint64_t {k}_k = 0; {k}_k < {k}_n; ++{k}_k) {{")
+        self.emit(f"const {it} {ivn} = ({it})((uint64_t){k}_lo + {k}_k * (uint64_t){k}_st);")
+        self.define(iv, ivn)
+        for a, nm in zip(carried, names):
+            self.define(a, nm)
+        self.gen_block(body)
+        self._assign_yield(body.ops[-1].operands, carried, names)
+        self.pop_scope()
         for r, nm in zip(op.results, names):
             self.define(r, nm)
 

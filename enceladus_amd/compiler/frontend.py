@@ -214,8 +214,34 @@ class CodeGenerator(ast.NodeVisitor):
             msg = self.visit(node.msg) if node.msg is not None else ""
             raise self.error(node, f"assertion failed: {msg}")
 
+    def visit_test(self, node):
+        """A condition whose truth value is all that matters (`if`, `x if c else y`,
+        `not`): `and`/`or` combine truth values there, so their operands may have
+        different types (reference: compiler/frontend.py:927-931). A compile-time false
+        (true) operand of `and` (`or`) decides the result without the later operands."""
+        if isinstance(node, ast.BoolOp):
+            kind = "and" if isinstance(node.op, ast.And) else "or"
+            acc = None
+            for v in node.values:
+                t = core.unwrap(self.visit_test(v))
+                if not is_value(t):
+                    if kind == "and" and not t:
+                        return False
+                    if kind == "or" and t:
+                        return True
+                    continue
+                acc = t if acc is None else semantic.binary(self.b, kind, acc, t)
+            return acc if acc is not None else kind == "and"
+        if isinstance(node, ast.UnaryOp) and isinstance(node.op, ast.Not):
+            t = core.unwrap(self.visit_test(node.operand))
+            return (not t) if not is_value(t) else semantic.binary(self.b, "eq", t, False)
+        x = core.unwrap(self.visit(node))
+        if not is_value(x) or x.type.shape or x.type.ptr or x.type.dtype.is_bool():
+            return x
+        return semantic.binary(self.b, "ne", x, 0)
+
     def visit_If(self, node):
-        cond = self.visit(node.test)
+        cond = self.visit_test(node.test)
         cond = core.unwrap(cond)
         if not is_value(cond):
             self.visit_stmts(node.body if cond else node.orelse)
@@ -353,8 +379,8 @@ class CodeGenerator(ast.NodeVisitor):
             if d in (core.int64, core.uint32, core.uint64):
                 dt = core.int64
         lo_v, hi_v, step_v = (semantic.cast(b, v, dt) for v in vals)
-        if isinstance(core.unwrap(step), int) and core.unwrap(step) <= 0:
-            raise self.error(node, "range() steps must be positive")
+        if isinstance(core.unwrap(step), int) and core.unwrap(step) == 0:
+            raise self.error(node, "range() arg 3 must not be zero")
         iv_name = node.target.id
         # Pass 1: find which names the body rebinds, and their types.
         assigned = [n for n in self._names_assigned(node.body) if n != iv_name]
@@ -425,9 +451,24 @@ class CodeGenerator(ast.NodeVisitor):
             self.scope[n] = r
         # As in Python, the loop variable keeps its last value after the loop, or its value
         # from before the loop when the loop doesn't run.
-        span = semantic.binary(b, "sub", semantic.binary(b, "sub", hi_v, lo_v), 1)
+        # last = lo + ((|hi - lo| - 1) // |step|) * step, for steps of either sign
+        cst = core.unwrap(step)
+        sub = lambda x, y: semantic.binary(b, "sub", x, y)  # noqa: E731
+        up = (sub(sub(hi_v, lo_v), 1), step_v)
+        down = (sub(sub(lo_v, hi_v), 1), sub(semantic.to_value(b, 0, dt), step_v))
+        if isinstance(cst, int):
+            num, den = up if cst > 0 else down
+            ran = semantic.binary(b, "lt", lo_v, hi_v) if cst > 0 else \
+                semantic.binary(b, "gt", lo_v, hi_v)
+        else:
+            pos = semantic.binary(b, "gt", step_v, 0)
+            num = semantic.select(b, pos, up[0], down[0])
+            den = semantic.select(b, pos, up[1], down[1])
+            ran = semantic.binary(b, "or", semantic.binary(
+                b, "and", pos, semantic.binary(b, "lt", lo_v, hi_v)), semantic.binary(
+                b, "and", semantic.binary(b, "lt", step_v, 0), semantic.binary(b, "gt", lo_v, hi_v)))
         last = semantic.binary(b, "add", lo_v, semantic.binary(
-            b, "mul", semantic.binary(b, "floordiv", span, step_v), step_v))
+            b, "mul", semantic.binary(b, "floordiv", num, den), step_v))
         prior = core.unwrap(self.scope.get(iv_name))
         if prior is not None:
             pdt = prior.type.dtype if is_value(prior) and not isinstance(prior.type, ir.DescType) \
@@ -436,7 +477,6 @@ class CodeGenerator(ast.NodeVisitor):
                 isinstance(prior, int) and not isinstance(prior, bool) and
                 semantic.adopt_literal(prior, dt) is dt)
             if same:
-                ran = semantic.binary(b, "lt", lo_v, hi_v)
                 last = semantic.select(b, ran, last, prior)
             else:
                 last = _Poison(f"`{iv_name}` is {prior!r} before the loop and an integer loop "
@@ -536,6 +576,9 @@ class CodeGenerator(ast.NodeVisitor):
         return self.binop(_BINOPS[type(node.op)], a, b_, node)
 
     def visit_UnaryOp(self, node):
+        if isinstance(node.op, ast.Not):
+            x = core.unwrap(self.visit_test(node.operand))
+            return (not x) if not is_value(x) else semantic.binary(self.b, "eq", x, 0)
         x = core.unwrap(self.visit(node.operand))
         if not is_value(x):
             if isinstance(node.op, ast.USub):
@@ -622,7 +665,7 @@ class CodeGenerator(ast.NodeVisitor):
         return val
 
     def visit_IfExp(self, node):
-        cond = core.unwrap(self.visit(node.test))
+        cond = core.unwrap(self.visit_test(node.test))
         if not is_value(cond):
             return self.visit(node.body) if cond else self.visit(node.orelse)
         return semantic.select(self.b, cond, self.visit(node.body), self.visit(node.orelse))

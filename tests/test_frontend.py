@@ -305,3 +305,23 @@ def test_errors_say_what_to_do(kernel, args, kw, phrase):
     lines, start = inspect.getsourcelines(kernel.fn)
     off = next(i for i, t in enumerate(lines) if t.rstrip().endswith("# error"))
     assert f"{__file__}:{start + off}:" in msg
+
+
+@enceladus.jit
+def _down_loop(out_ptr, n, f, STEP: tl.constexpr):
+    acc = 0
+    for i in range(n, 0, STEP):
+        acc += i
+    if (n and f) or not acc:      # truth values only: operand types may differ
+        acc += 1
+    tl.store(out_ptr, acc)
+
+
+def test_negative_steps_and_truth_contexts_lower():
+    import numpy as np
+    from enceladus_amd.compiler import codegen_hip
+    out = np.zeros(1, np.int32)
+    src = codegen_hip.generate(_down_loop.ir_for(out, 10, 0.5, STEP=-3)).source
+    assert "_n = " in src and "uint64_t" in src       # the trip-count loop form
+    with pytest.raises(enceladus.CompilationError, match="must not be zero"):
+        _down_loop.ir_for(out, 10, 0.5, STEP=0)
