@@ -3317,7 +3317,13 @@ def pack_args(kargs: list[KernelArg], values: list, pad8: bool = True) -> bytes:
             fmt, size = {"int32_t": ("i", 4), "int64_t": ("q", 8), "uint32_t": ("I", 4),
                          "uint64_t": ("Q", 8), "float": ("f", 4), "int16_t": ("h", 2),
                          "uint16_t": ("H", 2), "int8_t": ("b", 1), "uint8_t": ("B", 1)}[cp]
-            v = float(v) if fmt == "f" else int(v)
+            if fmt == "f":
+                # C's double -> float conversion (round to nearest even; beyond the float
+                # range, +-inf), which struct would refuse with OverflowError
+                with np.errstate(over="ignore"):
+                    v = float(np.float32(float(v)))
+            else:
+                v = int(v)
         pad = (-len(buf)) % size
         buf += b"\0" * pad
         buf += struct.pack("<" + fmt, v)

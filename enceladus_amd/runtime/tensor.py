@@ -18,54 +18,182 @@ from enceladus_amd.language import core
 from enceladus_amd.runtime import hip
 
 
-class Tensor:
-    """A contiguous device array owned by this runtime."""
+class _Allocation:
+    """One device allocation in HBM; freed when the last tensor viewing it goes away."""
 
-    def __init__(self, shape, dtype: core.dtype):
-        self.shape = tuple(int(s) for s in shape)
-        self.dtype = dtype
-        n = 1
-        for s in self.shape:
-            n *= s
-        self.numel = n
-        self.nbytes = n * dtype.itemsize
+    def __init__(self, nbytes: int):
         p = ctypes.c_void_p()
-        hip.call("ek_malloc", ctypes.byref(p), max(self.nbytes, 16))
+        hip.call("ek_malloc", ctypes.byref(p), max(int(nbytes), 16))
         self.ptr = p.value or 0
-        self._owner = True
-        s = 1
-        st = []
-        for d in reversed(self.shape):
-            st.append(s)
-            s *= d
-        self.strides = tuple(reversed(st))
-
-    def data_ptr(self) -> int:
-        return self.ptr
+        self.nbytes = int(nbytes)
 
     def __del__(self):
-        if getattr(self, "_owner", False) and self.ptr:
+        if getattr(self, "ptr", 0):
             try:
                 hip.call("ek_free", ctypes.c_void_p(self.ptr))
             except Exception:  # noqa: BLE001
                 pass
             self.ptr = 0
 
+
+class _Ptr(int):
+    """An address that reads both ways: `t.data_ptr` (the reference's property) and
+    `t.data_ptr()` (torch's method)."""
+
+    def __call__(self) -> int:
+        return int(self)
+
+
+def _contiguous(shape) -> tuple:
+    st, s = [], 1
+    for d in reversed(shape):
+        st.append(s)
+        s *= d
+    return tuple(reversed(st))
+
+
+class Tensor:
+    """A device array in HBM: an allocation plus shape, element strides and an element
+    offset, so that basic slicing gives views that share the allocation (reference:
+    runtime/tensor.py:65-233). Host access copies: `numpy()` reads the elements back,
+    `copy_()` writes them."""
+
+    def __init__(self, shape, dtype: core.dtype, strides=None, offset: int = 0,
+                 buffer: _Allocation | None = None):
+        if hasattr(shape, "ptr") and hasattr(shape, "nbytes"):
+            # the reference's order: Tensor(buffer, shape, dtype, strides=None, offset=0)
+            shape, dtype, strides, offset, buffer = dtype, strides, offset or None, \
+                buffer or 0, shape
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = _as_dtype(dtype)
+        self.strides = tuple(int(x) for x in strides) if strides is not None else \
+            _contiguous(self.shape)
+        self.offset = int(offset)
+        self.buffer = buffer if buffer is not None else \
+            _Allocation(self.numel * self.dtype.itemsize)
+
+    # ---- metadata ----
+    @property
+    def ndim(self) -> int:
+        return len(self.shape)
+
+    @property
+    def numel(self) -> int:
+        n = 1
+        for d in self.shape:
+            n *= d
+        return n
+
+    @property
+    def itemsize(self) -> int:
+        return self.dtype.itemsize
+
+    @property
+    def nbytes(self) -> int:
+        return self.numel * self.itemsize
+
+    @property
+    def byte_offset(self) -> int:
+        return self.offset * self.itemsize
+
+    @property
+    def ptr(self) -> int:
+        """The device address of the first element."""
+        return self.buffer.ptr + self.byte_offset
+
+    @property
+    def data_ptr(self) -> _Ptr:
+        return _Ptr(self.ptr)
+
+    def stride(self, dim: int | None = None):
+        """The stride of dimension `dim` in elements (all strides when `dim` is None)."""
+        return self.strides if dim is None else self.strides[dim]
+
+    def size(self, dim: int | None = None):
+        return self.shape if dim is None else self.shape[dim]
+
+    def is_contiguous(self) -> bool:
+        return self.strides == _contiguous(self.shape)
+
+    def __len__(self) -> int:
+        return self.shape[0]
+
+    # ---- host access ----
+    def _span(self) -> int:
+        """Elements from the first to one past the last (strides are non-negative)."""
+        if self.numel == 0:
+            return 0
+        return 1 + sum((n - 1) * st for n, st in zip(self.shape, self.strides))
+
+    def _host_window(self, span: int) -> np.ndarray:
+        w = np.empty(span, self.dtype.to_numpy())
+        if span:
+            from enceladus_amd.runtime import device
+            device.synchronize()
+            hip.call("ek_memcpy_d2h", w.ctypes.data_as(ctypes.c_void_p),
+                     ctypes.c_void_p(self.ptr), span * self.itemsize, None)
+        return w
+
+    def _as_view(self, w: np.ndarray) -> np.ndarray:
+        return np.lib.stride_tricks.as_strided(
+            w, self.shape, [st * self.itemsize for st in self.strides])
+
     def numpy(self) -> np.ndarray:
-        out = np.empty(self.shape, self.dtype.to_numpy())
-        if self.nbytes:
-            hip.call("ek_memcpy_d2h", out.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(self.ptr),
-                     self.nbytes, None)
-        return out
+        """Finishes pending GPU work and returns a host copy of the elements."""
+        if self.is_contiguous():
+            return self._host_window(self.numel).reshape(self.shape)
+        return np.array(self._as_view(self._host_window(self._span())))
+
+    def __array__(self, dtype=None, copy=None):
+        a = self.numpy()
+        return a.astype(dtype, copy=False) if dtype is not None else a
+
+    def tolist(self) -> list:
+        return self.numpy().tolist()
 
     def copy_from_numpy(self, a: np.ndarray) -> "Tensor":
-        a = np.ascontiguousarray(a)
-        if a.nbytes != self.nbytes:
-            raise ValueError("size mismatch")
-        if self.nbytes:
-            hip.call("ek_memcpy_h2d", ctypes.c_void_p(self.ptr), a.ctypes.data_as(ctypes.c_void_p),
-                     self.nbytes, None)
+        a = np.asarray(a, self.dtype.to_numpy())
+        if a.shape != self.shape and a.size != self.numel:
+            raise ValueError(f"size mismatch: {a.shape} into {self.shape}")
+        if not self.numel:
+            return self
+        if self.is_contiguous():
+            a = np.ascontiguousarray(a).reshape(-1)
+            hip.call("ek_memcpy_h2d", ctypes.c_void_p(self.ptr),
+                     a.ctypes.data_as(ctypes.c_void_p), self.nbytes, None)
+            hip.call("ek_device_sync")
+            return self
+        # a strided view: read its window, write the elements, write the window back
+        w = self._host_window(self._span())
+        self._as_view(w)[...] = a.reshape(self.shape)
+        hip.call("ek_memcpy_h2d", ctypes.c_void_p(self.ptr), w.ctypes.data_as(ctypes.c_void_p),
+                 w.nbytes, None)
+        hip.call("ek_device_sync")
         return self
+
+    def copy_(self, src: Any) -> "Tensor":
+        """Copies `src` (array-like, broadcast to this shape) into the tensor."""
+        return self.copy_from_numpy(np.broadcast_to(
+            np.asarray(src, self.dtype.to_numpy()), self.shape))
+
+    def __getitem__(self, key) -> "Tensor":
+        """A view sharing this tensor's allocation; basic slicing with positive steps."""
+        es = self.itemsize
+        probe = np.lib.stride_tricks.as_strided(
+            np.zeros(1, self.dtype.to_numpy()), self.shape, [st * es for st in self.strides],
+            writeable=False)
+        v = probe[key]
+        if not isinstance(v, np.ndarray) or (v.base is None and v.size):
+            raise TypeError("Tensor indexing supports only slices that give a view; use "
+                            ".numpy() to read single elements")
+        if v.size == 0:
+            return Tensor(v.shape, self.dtype, None, self.offset, self.buffer)
+        if any(x < 0 for x in v.strides):
+            raise ValueError("Tensor indexing doesn't support negative strides; index with "
+                             "a positive step")
+        off = (v.__array_interface__["data"][0] - probe.__array_interface__["data"][0]) // es
+        return Tensor(v.shape, self.dtype, tuple(x // es for x in v.strides),
+                      self.offset + off, self.buffer)
 
     def __repr__(self):
         return f"Tensor(shape={self.shape}, dtype={self.dtype})"

@@ -1,0 +1,156 @@
+"""Runtime behaviour around launches (reference test strategy: tests/test_runtime.py):
+views of device tensors, C conversion of float scalars, grid limits, 64-bit variants for
+arrays past 2^31 elements, and launches and synchronisations from several threads.
+CPU cases need no GPU; the rest are marked `gpu`."""
+
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+import enceladus
+import enceladus.language as tl
+from enceladus_amd.runtime.tensor import Tensor
+
+ROOT = __file__.rsplit("/tests/", 1)[0]
+
+
+class _BigBuffer:
+    """Stands in for a 16 GB allocation: only its metadata is read."""
+    ptr, nbytes = 1 << 20, 1 << 34
+
+
+def test_views_share_the_allocation_and_stay_inside_it():
+    t = Tensor(_BigBuffer(), (4, 6), "float32")
+    v = t[1:, ::2]
+    assert v.shape == (3, 3) and v.strides == (6, 2) and v.buffer is t.buffer
+    assert v.ptr == t.ptr + 6 * 4 and v.data_ptr == v.data_ptr() == v.ptr
+    assert not v.is_contiguous() and v.stride(1) == 2 and v.size(0) == 3 and len(v) == 3
+    for key in (slice(4, None), slice(2, 2)):
+        e = t[key]
+        assert e.numel == 0 and e.buffer is t.buffer
+        assert 0 <= e.byte_offset <= t.buffer.nbytes
+    with pytest.raises(TypeError):
+        t[1, 2]
+    with pytest.raises(ValueError, match="negative strides"):
+        t[:, ::-1]
+
+
+@enceladus.jit
+def _masked_tail(x_ptr, y_ptr, n, STEP: tl.constexpr, BLOCK: tl.constexpr):
+    pid = tl.program_id(0)
+    offs = pid * STEP + tl.arange(0, BLOCK)
+    local = offs - pid * STEP
+    tl.store(y_ptr + pid * BLOCK + local, tl.load(x_ptr + local) + 1.0, mask=offs < n)
+
+
+def test_arrays_past_2_31_elements_compile_a_64_bit_variant():
+    x = np.arange(16, dtype=np.float32)
+    n = (1 << 31) + 3
+    from enceladus_amd.compiler import widen
+    huge = Tensor(_BigBuffer(), ((1 << 31) + 1,), "float32")
+    assert not widen.needs_idx64(_masked_tail.ir_for(x, x, n, STEP=1 << 30, BLOCK=16))
+    assert widen.needs_idx64(_masked_tail.ir_for(huge, x, n, STEP=1 << 30, BLOCK=16))
+    big = _masked_tail.warmup(huge, x, n, STEP=1 << 30, BLOCK=16)
+    assert "(a0 + ((int64_t)" in big.hip            # 64-bit element offsets into x_ptr
+
+
+@enceladus.jit
+def _add_one(x_ptr, out_ptr, n, BLOCK: tl.constexpr):
+    offs = tl.program_id(0) * BLOCK + tl.arange(0, BLOCK)
+    m = offs < n
+    tl.store(out_ptr + offs, tl.load(x_ptr + offs, mask=m) + 1.0, mask=m)
+
+
+@pytest.mark.gpu
+def test_grids_past_the_hip_limits_are_refused():
+    x = np.ones(8, np.float32)
+    with pytest.raises(ValueError, match="exceeds the HIP limits"):
+        _add_one[(1 << 31,)](x, x, 8, BLOCK=8)
+    with pytest.raises(ValueError, match="exceeds the HIP limits"):
+        _add_one[(1, 70000)](x, x, 8, BLOCK=8)
+
+
+@pytest.mark.gpu
+def test_kernels_read_and_write_views():
+    print("[case] views", flush=True)
+    base = enceladus.zeros((8, 16))
+    host = np.arange(128, dtype=np.float32).reshape(8, 16)
+    base.copy_(host)
+    src = base[2:6]                                   # contiguous rows
+    out = enceladus.zeros((4, 16))
+    _add_one[(1,)](src, out, 64, BLOCK=64)
+    np.testing.assert_array_equal(out.numpy(), host[2:6] + 1)
+    col = base[:, 3:4]                                # a strided view reads back its elements
+    np.testing.assert_array_equal(col.numpy(), host[:, 3:4])
+    col.copy_(np.full((8, 1), -1.0, np.float32))      # and writes only them
+    want = host.copy()
+    want[:, 3] = -1
+    np.testing.assert_array_equal(base.numpy(), want)
+
+
+@enceladus.jit
+def _scale(out_ptr, a):
+    tl.store(out_ptr + tl.arange(0, 4), tl.full((4,), 1.0, tl.float32) * a)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("value", [1e40, -1e40, np.float64(1e39), 2.5])
+def test_float_scalars_convert_like_c(value):
+    print(f"[case] float scalar {value}", flush=True)
+    out = np.zeros(4, np.float32)
+    _scale[(1,)](out, value)
+    want = np.float32(value) if abs(value) < 3.4e38 else np.copysign(np.inf, value)
+    np.testing.assert_array_equal(out, want)
+
+
+_THREADS = """
+import sys, threading
+sys.path.insert(0, {root!r})
+import numpy as np
+import enceladus
+import enceladus.language as tl
+
+@enceladus.jit
+def inc(x_ptr, BLOCK: tl.constexpr):
+    offs = tl.program_id(0) * BLOCK + tl.arange(0, BLOCK)
+    tl.store(x_ptr + offs, tl.load(x_ptr + offs) + 1)
+
+ts = [enceladus.zeros(1024, dtype="int32") for _ in range(2)]
+inc[(4,)](ts[0], BLOCK=256)                  # compile once before the threads start
+enceladus.synchronize()
+ts[0].copy_(np.zeros(1024, np.int32))
+stop = threading.Event()
+def syncer():
+    while not stop.is_set():
+        enceladus.synchronize()
+def launch(t):
+    for _ in range({n}):
+        inc[(4,)](t, BLOCK=256)
+syncers = [threading.Thread(target=syncer) for _ in range(2)]
+launchers = [threading.Thread(target=launch, args=(t,)) for t in ts]
+for th in syncers + launchers:
+    th.start()
+for th in launchers:
+    th.join()
+stop.set()
+for th in syncers:
+    th.join()
+enceladus.synchronize()
+for t in ts:
+    np.testing.assert_array_equal(t.numpy(), {n})
+print("ok", flush=True)
+"""
+
+
+@pytest.mark.gpu
+def test_concurrent_launches_and_syncs(tmp_path):
+    # its own process, so that a failure ends only this test (a file: the kernel's source
+    # must be readable)
+    print("[case] threads", flush=True)
+    script = tmp_path / "threads.py"
+    script.write_text(_THREADS.format(root=ROOT, n=5000))
+    r = subprocess.run([sys.executable, str(script)], capture_output=True, timeout=100)
+    assert r.returncode == 0, r.stderr.decode()[-2000:]
+    assert b"ok" in r.stdout
