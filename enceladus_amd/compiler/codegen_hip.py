@@ -624,7 +624,11 @@ class Emitter:
             if k in ("eq", "ne", "lt", "le", "gt", "ge"):
                 return f"({a} {_INFIX[k]} {b})"
             cdt = "float" if is_half(dt) else ctype(dt)
-            if k in ("add", "sub", "mul", "div"):
+            if k in ("add", "sub", "mul") and dt in (core.int32, core.int64):
+                # signed 32/64-bit math wraps (two's complement), as the language defines
+                # it; C++ leaves signed overflow undefined
+                e = f"ek::w{k}({a}, {b})"
+            elif k in ("add", "sub", "mul", "div"):
                 e = f"({a} {_INFIX[k]} {b})"
             elif k in ("and", "or", "xor"):
                 e = f"({a} {_INFIX[k]} {b})"
@@ -667,8 +671,11 @@ class Emitter:
                     e = f"{_MATH[k]}({fa})"
                 return f"ek::rnd<{ctype(dt)}>({e})" if is_half(dt) else e
             if k == "neg":
-                return f"(({ctype(dt)})(-{a}))"
+                return f"ek::wneg({a})" if dt in (core.int32, core.int64) else \
+                    f"(({ctype(dt)})(-{a}))"
             if k == "abs":
+                if dt in (core.int32, core.int64):
+                    return f"({a} < 0 ? ek::wneg({a}) : {a})"
                 return f"(({ctype(dt)})({a} < 0 ? -{a} : {a}))"
             raise CompilationError(f"`{k}` needs a floating-point input")
         if n == "cast":

@@ -13,6 +13,8 @@ from __future__ import annotations
 
 import ast
 import builtins
+import sys
+import types
 import inspect
 import textwrap
 from typing import Any
@@ -74,6 +76,18 @@ class Context:
         self.b = b
         self.num_warps = num_warps
         self.options = options
+        # what the kernel read at compile time outside its arguments: (container, name,
+        # value, is_mapping); a launch recompiles when one of them changed (reference:
+        # runtime/jit.py:289, 1037-1234)
+        self.deps: list = []
+        self._dep_seen: set = set()
+
+    def record(self, container, name: str, value, mapping: bool) -> None:
+        key = (id(container), name)
+        if key in self._dep_seen or isinstance(value, types.ModuleType):
+            return
+        self._dep_seen.add(key)
+        self.deps.append((container, name, value, mapping))
 
     def is_known_one(self, v) -> bool:
         v = core.unwrap(v)
@@ -99,10 +113,12 @@ class CodeGenerator(ast.NodeVisitor):
         self.ctx = ctx
         self.fn = fn
         self.globals = dict(fn.__globals__)
+        self._cells: dict = {}
         if fn.__closure__:
             for name, cell in zip(fn.__code__.co_freevars, fn.__closure__):
                 try:
                     self.globals[name] = cell.cell_contents
+                    self._cells[name] = cell
                 except ValueError:
                     pass
         self.scope = scope
@@ -502,6 +518,10 @@ class CodeGenerator(ast.NodeVisitor):
             return v
         if name in self.globals:
             v = self.globals[name]
+            if name in self._cells:
+                self.ctx.record(self._cells[name], "cell_contents", v, False)
+            else:
+                self.ctx.record(self.fn.__globals__, name, v, True)
             return v
         if hasattr(builtins, name):
             return getattr(builtins, name)
@@ -536,9 +556,12 @@ class CodeGenerator(ast.NodeVisitor):
         if is_value(obj):
             return value_attr(self.ctx, obj, attr)
         try:
-            return getattr(obj, attr)
+            v = getattr(obj, attr)
         except AttributeError as e:
             raise self.error(node, str(e)) from None
+        if isinstance(obj, (types.ModuleType, type)) and not _stable_module(obj):
+            self.ctx.record(obj, attr, v, False)
+        return v
 
     def visit_Subscript(self, node):
         obj = core.unwrap(self.visit(node.value))
@@ -710,6 +733,14 @@ class CodeGenerator(ast.NodeVisitor):
             raise self.error(node, f"`{getattr(fn, '__name__', fn)}` can't take runtime values")
         if fn is builtins.print:
             return None
+        code = getattr(fn, "__code__", None)
+        glb = getattr(fn, "__globals__", None)
+        if code is not None and glb is not None and not _stable_module(
+                sys.modules.get(getattr(fn, "__module__", ""), None)):
+            # a plain Python helper runs now: the globals it names are dependencies too
+            for nm in code.co_names:
+                if nm in glb:
+                    self.ctx.record(glb, nm, glb[nm], True)
         return fn(*[core.unwrap(a) for a in args],
                    **{k: core.unwrap(v) for k, v in kwargs.items()})
 
@@ -870,4 +901,13 @@ def build_ir(fn, arg_types: dict[str, Any], arg_facts: dict[str, dict], constexp
                 raise gen.error(r.node, "kernels can't return values; store results through "
                                         "a pointer argument") from None
             raise CompilationError("kernels can't return values") from None
-    return ir.Func(fn.__name__, args, names, body, num_warps, dict(options or {}))
+    f = ir.Func(fn.__name__, args, names, body, num_warps, dict(options or {}))
+    f.deps = ctx.deps
+    return f
+
+
+def _stable_module(m) -> bool:
+    """The language's and the runtime's own modules: their attributes don't change."""
+    name = getattr(m, "__name__", "") or ""
+    return name.split(".")[0] in ("enceladus", "enceladus_amd", "numpy", "math", "builtins")
+

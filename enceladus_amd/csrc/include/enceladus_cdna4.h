@@ -507,6 +507,17 @@ EK_INLINE void assert_fail(uint32_t* buf, int index, int px, int py, int pz) {
     __hip_atomic_store(buf + 4, (uint32_t)pz, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
+// Two's-complement wrapping add/sub/mul/neg for the language's signed 32/64-bit integers
+// (signed overflow is undefined in C++).
+EK_INLINE int32_t wadd(int32_t a, int32_t b) { return (int32_t)((uint32_t)a + (uint32_t)b); }
+EK_INLINE int32_t wsub(int32_t a, int32_t b) { return (int32_t)((uint32_t)a - (uint32_t)b); }
+EK_INLINE int32_t wmul(int32_t a, int32_t b) { return (int32_t)((uint32_t)a * (uint32_t)b); }
+EK_INLINE int32_t wneg(int32_t a) { return (int32_t)(0u - (uint32_t)a); }
+EK_INLINE int64_t wadd(int64_t a, int64_t b) { return (int64_t)((uint64_t)a + (uint64_t)b); }
+EK_INLINE int64_t wsub(int64_t a, int64_t b) { return (int64_t)((uint64_t)a - (uint64_t)b); }
+EK_INLINE int64_t wmul(int64_t a, int64_t b) { return (int64_t)((uint64_t)a * (uint64_t)b); }
+EK_INLINE int64_t wneg(int64_t a) { return (int64_t)(0ull - (uint64_t)a); }
+
 // Atomic read-modify-write as a compare-and-swap loop: `f(old)` gives the new value. Used for
 // the updates without a native instruction: float max/min, value-compare CAS on floats, and
 // every 8- and 16-bit element, which is updated inside its aligned 32-bit word (the CAS

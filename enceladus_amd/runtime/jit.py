@@ -15,6 +15,7 @@ from __future__ import annotations
 import ctypes
 import inspect
 import os
+import struct
 from dataclasses import dataclass
 from typing import Any, Callable
 
@@ -164,15 +165,43 @@ def _writes(fn: ir.Func) -> set[int]:
     return out
 
 
+_MISSING = object()
+
+
+def _same(a, b) -> bool:
+    if a is b:
+        return True
+    if type(a) is not type(b):
+        return False
+    if isinstance(a, float):
+        return struct.pack("<d", a) == struct.pack("<d", b)
+    if isinstance(a, (tuple, list)):
+        return len(a) == len(b) and all(_same(x, y) for x, y in zip(a, b))
+    if isinstance(a, (int, str, bytes, bool, complex)):
+        return a == b
+    return False
+
+
 class Launcher:
     """A compiled kernel plus the per-specialization launch plan."""
 
     def __init__(self, ck: C.CompiledKernel, runtime_names: list[str], writes: set[int],
-                 constexprs: dict):
+                 constexprs: dict, deps: list | None = None):
         self.ck = ck
         self.runtime_names = runtime_names
         self.writes = writes
         self.constexprs = constexprs
+        self.deps = list(deps or ())
+
+    def current(self) -> bool:
+        """Whether every global, module or class attribute the compile read still holds
+        the value it read (floats by bit pattern, so 0.0 -> -0.0 is a change)."""
+        for container, name, value, mapping in self.deps:
+            now = container.get(name, _MISSING) if mapping else \
+                getattr(container, name, _MISSING)
+            if not _same(now, value):
+                return False
+        return True
 
     def __call__(self, grid, values: list, stream: int | None = None):
         bindings = []
@@ -285,7 +314,11 @@ class JITFunction:
             if isinstance(v, core.dtype):
                 return ("dt", v.name)
             if isinstance(v, (list, tuple)):
-                return tuple(ck(x) for x in v)
+                return (type(v).__name__,) + tuple(ck(x) for x in v)
+            if isinstance(v, float):
+                # by bit pattern: 0.0 and -0.0 give different kernels, and one NaN
+                # launch reuses another's kernel
+                return ("float", struct.pack("<d", v))
             return (type(v).__name__, v)
         return (tuple((k, str(t)) for k, t in types.items()),
                 tuple((k, tuple(sorted(f.items()))) for k, f in facts.items()),
@@ -304,7 +337,7 @@ class JITFunction:
         fn_ir = C.build_module(self, types, facts, consts, num_warps, options)
         ck = C.compile_ir(fn_ir, options)
         runtime_names = list(types.keys())
-        return Launcher(ck, runtime_names, _writes(fn_ir), consts)
+        return Launcher(ck, runtime_names, _writes(fn_ir), consts, getattr(fn_ir, "deps", ()))
 
     def _lookup(self, vals, num_warps, dot_warps) -> Launcher:
         types, facts, consts = self.specialize(vals)
@@ -312,7 +345,7 @@ class JITFunction:
                os.environ.get("ENCELADUS_CODEGEN", ""),
                os.environ.get("ENCELADUS_OVERRIDE_DIR", ""), _debug())
         lc = self._cache.get(key)
-        if lc is None:
+        if lc is None or (lc.deps and not lc.current()):
             lc = self._compile_for(types, facts, consts, num_warps, dot_warps)
             self._cache[key] = lc
         return lc

@@ -154,3 +154,93 @@ def test_concurrent_launches_and_syncs(tmp_path):
     r = subprocess.run([sys.executable, str(script)], capture_output=True, timeout=100)
     assert r.returncode == 0, r.stderr.decode()[-2000:]
     assert b"ok" in r.stdout
+
+
+# -- the launch cache and what a kernel read at compile time --------------------------
+
+SCALE = 2.0
+TUP = (2.0, 3.0)
+ZERO = 0.0
+FACTOR = 4.0
+
+
+def _python_factor():
+    return FACTOR
+
+
+@enceladus.jit
+def _helper(x):
+    return x * SCALE
+
+
+@enceladus.jit
+def _scale_by_globals(x_ptr, out_ptr):
+    offs = tl.arange(0, 16)
+    x = tl.load(x_ptr + offs)
+    tl.store(out_ptr + offs, _helper(x) + TUP[1] + _python_factor() + 1.0 / (x * 0.0 + ZERO))
+
+
+def _globals_reference(x):
+    with np.errstate(divide="ignore"):
+        return x * SCALE + TUP[1] + FACTOR + 1.0 / (x * 0.0 + ZERO)
+
+
+@pytest.mark.parametrize("name,value", [("SCALE", 5.0), ("TUP", (2.0, 7.0)), ("FACTOR", 9.0),
+                                        ("ZERO", -0.0)])
+def test_changed_globals_recompile(name, value, monkeypatch):
+    x = np.arange(1, 17, dtype=np.float32)
+    first = _scale_by_globals.warmup(x, x)
+    assert first is _scale_by_globals.warmup(x, x)          # warm: the same kernel
+    monkeypatch.setitem(globals(), name, value)
+    assert _scale_by_globals.warmup(x, x) is not first      # the read value changed
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,value", [("SCALE", 5.0), ("TUP", (2.0, 7.0)), ("FACTOR", 9.0),
+                                        ("ZERO", -0.0)])
+def test_changed_globals_give_new_results(name, value, monkeypatch):
+    print(f"[case] global {name}", flush=True)
+    x = np.arange(1, 17, dtype=np.float32)
+    out = np.empty(16, np.float32)
+    _scale_by_globals[(1,)](x, out)
+    np.testing.assert_array_equal(out, _globals_reference(x))
+    monkeypatch.setitem(globals(), name, value)
+    _scale_by_globals[(1,)](x, out)
+    np.testing.assert_array_equal(out, _globals_reference(x))
+
+
+@enceladus.jit
+def _reciprocal(out_ptr, C: tl.constexpr):
+    offs = tl.arange(0, 16)
+    tl.store(out_ptr + offs, 1.0 / (tl.full((16,), 1.0, tl.float32) * C))
+
+
+@pytest.mark.gpu
+def test_float_constexprs_are_keyed_by_bit_pattern():
+    print("[case] float constexpr keys", flush=True)
+    out = np.empty(16, np.float32)
+    got, sizes = [], []
+    for c in (0.0, -0.0, float("nan"), float("nan")):
+        _reciprocal[(1,)](out, C=c)
+        got.append(out[0])
+        sizes.append(len(_reciprocal._cache))
+    np.testing.assert_array_equal(got, [np.inf, -np.inf, np.nan, np.nan])
+    assert sizes[3] == sizes[2]
+
+
+@enceladus.jit
+def _scaled(out_ptr, S: tl.constexpr):
+    offs = tl.arange(0, 16)
+    tl.store(out_ptr + offs, (offs + 2147483647) * S)
+
+
+@pytest.mark.gpu
+def test_constexprs_that_compare_equal_compile_separately():
+    # 2 == 2.0 and 1 == True, but int32 math wraps and float math doesn't
+    from oracle import interpreter as O
+    print("[case] equal constexprs", flush=True)
+    for s in (2, 2.0, 1, True):
+        got, want = np.zeros(16, np.float32), np.zeros(16, np.float32)
+        _scaled[(1,)](got, S=s)
+        O.run_grid(_scaled, (1,), want, S=s)
+        np.testing.assert_array_equal(got, want)
