@@ -47,6 +47,12 @@ _INFIX = {"add": "+", "sub": "-", "mul": "*", "div": "/", "and": "&", "or": "|",
           "eq": "==", "ne": "!=", "lt": "<", "le": "<=", "gt": ">", "ge": ">="}
 
 
+def _through_trans(v: ir.Value) -> ir.Value:
+    while v.op is not None and v.op.name == "trans":
+        v = v.op.operands[0]
+    return v
+
+
 def ctype(dt: core.dtype) -> str:
     return dt.cname
 
@@ -144,12 +150,15 @@ class GeneratedKernel:
     # indices), "total" (words per workgroup row of the partial buffer), "chunks" (64-word
     # column chunks)}; the launcher runs `name` on grid (chunks, rows / rb) after the kernel
     flush: dict | None = None
+    # what `kernel.explain` reports: {"conversions", "lds", "dots"} recorded by the emitter
+    report: dict = field(default_factory=dict)
 
 
 class Emitter:
     def __init__(self, fn: ir.Func, options: dict | None = None):
         self.fn = fn
         self.opt = options or {}
+        self.report: dict = {}
         self.nw = fn.num_warps
         self.nt = 64 * self.nw
         self.axis = AxisAnalysis(fn)
@@ -185,6 +194,10 @@ class Emitter:
         self.cur.items.append(self.cur.indent + line)
 
     def need_lds(self, nbytes: int):
+        op = getattr(self, "cur_op", None)
+        if op is not None:
+            self.report.setdefault("lds", []).append(
+                {"op": op.name, "loc": op.loc, "bytes": int(nbytes)})
         self.lds = max(self.lds, nbytes)
         if getattr(self, "in_staged_loop", 0):
             self.scratch_in_stage_loop = True
@@ -890,6 +903,10 @@ class Emitter:
             raise CompilationError(f"a layout conversion of a {a.shape} tile needs {nbytes} "
                                    "bytes of LDS")
         self.need_lds(nbytes)
+        op = getattr(self, "cur_op", None)
+        self.report.setdefault("conversions", []).append(
+            {"value": src, "loc": op.loc if op is not None else None, "bytes": int(nbytes),
+             "src": a, "dst": dst})
         nm = self.fresh("cv")
         sname = self.name[src.id]
         lines = []
@@ -946,6 +963,14 @@ class Emitter:
             self.gen_op(op)
 
     def gen_op(self, op: ir.Op):
+        prev = getattr(self, "cur_op", None)
+        self.cur_op = op
+        try:
+            self._gen_op(op)
+        finally:
+            self.cur_op = prev
+
+    def _gen_op(self, op: ir.Op):
         n = op.name
         fn = getattr(self, f"op_{n}", None)
         if n in ("yield",):
@@ -2167,6 +2192,10 @@ class Emitter:
         la, lb = LY.mfma_operand(plan, "a"), LY.mfma_operand(plan, "b")
         lc = self.lay[res.id]
         ins = plan.inst
+        self.report.setdefault("dots", []).append(
+            {"loc": op.loc, "plan": plan, "staged": [o for o, st in (("a", a), ("b", b))
+                                                     if _through_trans(st).id in
+                                                     getattr(self, "staged", {})]})
         sa = self._staged_operand(a, la)
         sb = self._staged_operand(b, lb)
         aa = None if sa else self.array(a, la)
@@ -2775,6 +2804,7 @@ class Emitter:
                 "scalar_ops": scalar_ops, "dt": dt, "bm": bm, "bn": bn, "bk": bk}
 
     def _emit_gemm_loop(self, op, g) -> bool:
+        self.report["gemm_template"] = op.loc
         body = op.regions[0]
         acc_arg = body.args[1]
         init = op.operands[3]
@@ -3269,6 +3299,7 @@ class Emitter:
         gk.coarsen = int(self.coarsen)
         gk.asserts = list(self.asserts)
         gk.flush = flush
+        gk.report = self.report
         return gk
 
 

@@ -180,6 +180,9 @@ class CodeGenerator(ast.NodeVisitor):
 
     def assign_target(self, target, value, node):
         if isinstance(target, ast.Name):
+            v = core.unwrap(value)
+            if isinstance(v, ir.Value) and not v.name_hint and v.op is not None:
+                v.name_hint = target.id          # for kernel.explain's report
             self.scope[target.id] = value
         elif isinstance(target, (ast.Tuple, ast.List)):
             vals = core.unwrap(value)

@@ -382,10 +382,16 @@ class JITFunction:
                               {"dot_warps": tuple(dot_warps) if dot_warps else None,
                                "debug": _debug()})
 
-    def explain(self, *args, **kwargs) -> str:
+    def explain(self, *args, grid=None, full: bool = False, **kwargs) -> str:
+        """A report of the compiler's decisions for the specialization these arguments
+        select (reference: runtime/jit.py:539): MFMA plans, layout conversions and LDS
+        by source line. `full=True` appends the IR and the generated HIP."""
+        from enceladus_amd.compiler import explain as EX
         ck = self.warmup(*args, **kwargs)
-        return (f"kernel {ck.name}: num_warps={ck.num_warps} lds={ck.lds_bytes}B\n"
-                f"--- IR ---\n{ck.ir}\n--- HIP ---\n{ck.hip}")
+        text = EX.explain(ck, grid)
+        if full:
+            text += f"\n\n--- IR ---\n{ck.ir}\n--- HIP ---\n{ck.hip}"
+        return text
 
 
 def jit(fn=None, *, interpret=None, do_not_specialize=(), math_mode: str = "relaxed"):
