@@ -110,7 +110,8 @@ def dtype_from_numpy(np_dtype: Any) -> dtype:
     if name is not None:
         return _BY_NAME[name]
     if d == np.float64:
-        raise TypeError("Enceladus has no float64 type. Cast the array to float32 first.")
+        raise TypeError("Enceladus has no float64 type. Cast the array to float32 first "
+                        "(for example `x.astype(np.float32)`, or `x.float()` for torch).")
     raise TypeError(f"NumPy dtype {d} has no Enceladus equivalent.")
 
 

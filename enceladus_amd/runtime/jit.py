@@ -291,7 +291,8 @@ class JITFunction:
         for p in self.params:
             if p.name not in vals:
                 if p.default is inspect.Parameter.empty:
-                    raise TypeError(f"{self.__name__} is missing argument `{p.name}`")
+                    raise TypeError(f"{self.__name__}: missing a required argument: "
+                                    f"'{p.name}'")
                 vals[p.name] = p.default
         return vals
 
@@ -300,9 +301,19 @@ class JITFunction:
         for p in self.params:
             v = vals[p.name]
             if p.is_constexpr:
-                consts[p.name] = core.unwrap(v)
+                c = core.unwrap(v)
+                try:
+                    hash(c if not isinstance(c, list) else tuple(c))
+                except TypeError:
+                    raise TypeError(f"{self.__name__}: constexpr parameter `{p.name}` got an "
+                                    f"unhashable {type(c).__name__}; pass a number, a string, "
+                                    "a dtype or a tuple of those") from None
+                consts[p.name] = c
                 continue
-            types[p.name] = arg_type(v)
+            try:
+                types[p.name] = arg_type(v)
+            except TypeError as e:
+                raise TypeError(f"{self.__name__}: argument `{p.name}`: {e}") from None
             f = arg_facts(v)
             if p.do_not_specialize:
                 f = {k: x for k, x in f.items() if k in REQUIRED_FACTS}

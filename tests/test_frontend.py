@@ -325,3 +325,22 @@ def test_negative_steps_and_truth_contexts_lower():
     assert "_n = " in src and "uint64_t" in src       # the trip-count loop form
     with pytest.raises(enceladus.CompilationError, match="must not be zero"):
         _down_loop.ir_for(out, 10, 0.5, STEP=0)
+
+
+@enceladus.jit
+def _fill(x_ptr, BLOCK: tl.constexpr):
+    tl.store(x_ptr + tl.arange(0, 16), 1.0)
+
+
+@pytest.mark.parametrize("args,kwargs,phrases", [
+    (lambda: (np.zeros(64),), {"BLOCK": 16}, ["argument `x_ptr`", "astype(np.float32)"]),
+    (lambda: (np.zeros(64, np.float32),), {}, ["missing a required argument: 'BLOCK'"]),
+    (lambda: (np.zeros(64, np.float32),), {"BLOCK": {16: 16}}, ["parameter `BLOCK`", "a tuple"]),
+])
+def test_bad_arguments_name_the_kernel_and_argument(args, kwargs, phrases):
+    with pytest.raises(TypeError) as e:
+        _fill.warmup(*args(), **kwargs)
+    msg = str(e.value)
+    assert msg.startswith("_fill: ")
+    for p in phrases:
+        assert p in msg
