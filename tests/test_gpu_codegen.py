@@ -221,3 +221,37 @@ def test_float_comparisons_follow_ieee_nan_rules(dtype):
     want = sum(p.astype(np.int32) << i for i, p in enumerate(preds))
     np.testing.assert_array_equal(bits, np.append(want, 1).astype(np.int32))
     np.testing.assert_array_equal(sel, np.where(x == x, x, -1).astype(dtype))
+
+
+@enceladus.jit
+def _scale_rows(x_ptr, y_ptr, M, N, sx, sy, BM: tl.constexpr, BN: tl.constexpr):
+    rm = tl.program_id(0) * BM + tl.arange(0, BM)
+    rn = tl.arange(0, BN)
+    mask = (rm[:, None] < M) & (rn[None, :] < N)
+    x = tl.load(x_ptr + rm[:, None] * sx + rn[None, :], mask=mask, other=3)
+    tl.store(y_ptr + rm[:, None] * sy + rn[None, :], x * 2 + 1, mask=mask)
+
+
+# (case, M, N, x row stride, x offset into its allocation): aligned rows; rows that start
+# at unaligned addresses; a view one element into its allocation; a mask that changes
+# inside a vector
+ROWS = [("aligned", 20, 64, 64, 0), ("odd_stride", 20, 64, 65, 0),
+        ("offset_view", 20, 64, 64, 1), ("ragged_cols", 20, 50, 64, 0)]
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16", "int8", "int64"])
+@pytest.mark.parametrize("case,m,n,sx,off", ROWS, ids=[r[0] for r in ROWS])
+def test_vector_accesses_match_scalar_ones(dtype, case, m, n, sx, off):
+    # device views, so that unaligned rows and offsets reach the kernel as they are
+    import torch
+    print(f"[case] vector accesses {case} {dtype}", flush=True)
+    td = getattr(torch, dtype)
+    rng = np.random.default_rng(34)
+    base = torch.from_numpy(rng.integers(-50, 50, off + m * sx + 8)).to(td).cuda()
+    x = base[off:off + m * sx].view(m, sx)
+    y = torch.zeros((m, 64), dtype=td, device="cuda")
+    _scale_rows[(enceladus.cdiv(m, 8),)](x, y, m, n, sx, 64, BM=8, BN=64)
+    torch.cuda.synchronize()
+    want = torch.zeros((m, 64), dtype=td)
+    want[:, :n] = x.cpu()[:, :n] * 2 + 1
+    assert torch.equal(y.cpu(), want)
