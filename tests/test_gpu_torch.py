@@ -199,3 +199,50 @@ def test_writes_to_read_only_numpy_arrays_are_refused():
     with pytest.raises(ValueError, match="read-only NumPy array"):
         add_kernel[(1,)](host, host, np.broadcast_to(np.zeros(1, np.float32), (8,)), 8, BLOCK=8)
     assert not np.frombuffer(ro.tobytes(), np.float32).any()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("example", ["softmax", "rmsnorm", "vector_add"])
+def test_math_is_bit_identical_across_launch_paths(example):
+    # NumPy (copied in and out), torch-ROCm and enceladus.Tensor arguments select the same
+    # specialization, so the results agree bit for bit (reference test strategy:
+    # tests/test_interop.py test_math_is_bit_identical_across_launch_paths)
+    import torch
+    import enceladus
+    print(f"[case] launch paths {example}", flush=True)
+    rng = np.random.default_rng(40)
+    if example == "vector_add":
+        from examples.vector_add import add_kernel
+        x, y = (rng.standard_normal(5000).astype(np.float32) for _ in range(2))
+        run = lambda a, b, o: add_kernel[(5,)](a, b, o, 5000, BLOCK=1024)  # noqa: E731
+        shape = (5000,)
+    elif example == "softmax":
+        from examples.softmax import softmax_kernel
+        x, y = rng.standard_normal((16, 1000)).astype(np.float32), None
+        run = lambda a, b, o: softmax_kernel[(16,)](o, a, 1000, 1000, 1000,  # noqa: E731
+                                                     BLOCK=1024)
+        shape = (16, 1000)
+    else:
+        from examples.rmsnorm import rmsnorm_kernel
+        x = rng.standard_normal((16, 1000)).astype(np.float32)
+        y = rng.uniform(0.5, 1.5, 1000).astype(np.float32)
+        run = lambda a, b, o: rmsnorm_kernel[(16,)](a, b, o, 1000, 1000, 1000, 1e-6,  # noqa: E731
+                                                     BLOCK=1024)
+        shape = (16, 1000)
+    outs = []
+    o = np.zeros(shape, np.float32)
+    run(x, y, o)
+    outs.append(o)
+    tx = torch.from_numpy(x).cuda()
+    ty = torch.from_numpy(y).cuda() if y is not None else None
+    to = torch.zeros(shape, dtype=torch.float32, device="cuda")
+    run(tx, ty, to)
+    torch.cuda.synchronize()
+    outs.append(to.cpu().numpy())
+    ex = enceladus.from_numpy(x)
+    ey = enceladus.from_numpy(y) if y is not None else None
+    eo = enceladus.zeros(shape)
+    run(ex, ey, eo)
+    outs.append(eo.numpy())
+    assert outs[0].view(np.uint32).tolist() == outs[1].view(np.uint32).tolist()
+    assert outs[0].view(np.uint32).tolist() == outs[2].view(np.uint32).tolist()
