@@ -284,3 +284,104 @@ def test_debug_barrier_orders_stores_before_loads_by_other_threads(num_warps):
     out = np.zeros(1024, np.int32)
     _barrier_kernel[(1,)](buf, out, BLOCK=1024, num_warps=num_warps)
     np.testing.assert_array_equal(out, (1023 - np.arange(1024)) * 3)
+
+
+# -- scans over every layout kind (reference: tests/test_atomics_scans.py:228-339) ----
+
+@enceladus.jit
+def _max_op(a, b):
+    return tl.maximum(a, b)
+
+
+@enceladus.jit
+def _affine_op(a0, a1, b0, b1):
+    # composes h -> a0 * h + a1, then h -> b0 * h + b1: associative, not commutative
+    return a0 * b0, b0 * a1 + b1
+
+
+@enceladus.jit
+def _scan2d_kernel(a_ptr, b_ptr, x_ptr, y_ptr, M: tl.constexpr, N: tl.constexpr,
+                   AXIS: tl.constexpr, REVERSE: tl.constexpr):
+    offs = tl.arange(0, M)[:, None] * N + tl.arange(0, N)[None, :]
+    a, b = tl.load(a_ptr + offs), tl.load(b_ptr + offs)
+    h0, h1 = tl.associative_scan((a, b), AXIS, _affine_op, reverse=REVERSE)
+    tl.store(a_ptr + offs, h0)
+    tl.store(b_ptr + offs, h1)
+    x = tl.load(x_ptr + offs)
+    tl.store(y_ptr + offs, tl.associative_scan(x, AXIS, _max_op, reverse=REVERSE))
+
+
+def _affine_ref(a, b, axis, reverse):
+    a, b = np.moveaxis(a, axis, 0).copy(), np.moveaxis(b, axis, 0).copy()
+    order = range(a.shape[0] - 2, -1, -1) if reverse else range(1, a.shape[0])
+    prev = a.shape[0] - 1 if reverse else 0
+    for i in order:
+        a[i], b[i] = a[prev] * a[i], a[i] * b[prev] + b[i]
+        prev = i
+    return np.moveaxis(a, 0, axis), np.moveaxis(b, 0, axis)
+
+
+@pytest.mark.parametrize("m,n", [(16, 64), (64, 16), (8, 2)])
+@pytest.mark.parametrize("axis", [0, 1])
+@pytest.mark.parametrize("reverse", [False, True])
+def test_associative_scan_along_either_axis_of_a_2d_tile(m, n, axis, reverse):
+    _say(f"scan2d {m}x{n} axis={axis} reverse={reverse}")
+    rng = np.random.default_rng(m * n + axis)
+    a = rng.integers(-3, 4, (m, n)).astype(np.int32)        # int32 wraps exactly in any order
+    b = rng.integers(-100, 100, (m, n)).astype(np.int32)
+    x = rng.standard_normal((m, n)).astype(np.float32)
+    ga, gb, y = a.copy(), b.copy(), np.empty_like(x)
+    _scan2d_kernel[(1,)](ga, gb, x, y, M=m, N=n, AXIS=axis, REVERSE=reverse)
+    with np.errstate(over="ignore"):
+        wa, wb = _affine_ref(a, b, axis, reverse)
+    f = np.flip if reverse else (lambda z, axis: z)
+    np.testing.assert_array_equal(ga, wa)
+    np.testing.assert_array_equal(gb, wb)
+    np.testing.assert_array_equal(y, f(np.maximum.accumulate(f(x, axis=axis), axis=axis),
+                                       axis=axis))
+
+
+@enceladus.jit
+def _dot_cumsum_kernel(a_ptr, b_ptr, out_ptr, M: tl.constexpr, N: tl.constexpr,
+                       K: tl.constexpr, AXIS: tl.constexpr):
+    rm, rn, rk = tl.arange(0, M), tl.arange(0, N), tl.arange(0, K)
+    a = tl.load(a_ptr + rm[:, None] * K + rk[None, :])
+    b = tl.load(b_ptr + rk[:, None] * N + rn[None, :])
+    c = tl.cumsum(tl.dot(a, b), axis=AXIS)
+    tl.store(out_ptr + rm[:, None] * N + rn[None, :], c)
+
+
+@pytest.mark.parametrize("axis", [0, 1])
+def test_cumsum_of_a_dot_accumulator(axis):
+    # the MFMA accumulator layout interleaves register and lane bits along both axes
+    _say(f"cumsum of dot axis={axis}")
+    rng = np.random.default_rng(axis)
+    a = rng.integers(-2, 3, (64, 16)).astype(np.float32)
+    b = rng.integers(-2, 3, (16, 32)).astype(np.float32)
+    out = np.empty((64, 32), np.float32)
+    _dot_cumsum_kernel[(1,)](a, b, out, M=64, N=32, K=16, AXIS=axis)
+    np.testing.assert_array_equal(out, np.cumsum(a @ b, axis=axis))
+
+
+@enceladus.jit
+def _view_scan_kernel(a_ptr, b_ptr, out_a, out_b, REVERSE: tl.constexpr):
+    offs = tl.arange(0, 2)[:, None] * 256 + tl.arange(0, 256)[None, :]
+    a = tl.reshape(tl.trans(tl.load(a_ptr + offs)), (512,))
+    b = tl.reshape(tl.trans(tl.load(b_ptr + offs)), (512,))
+    h0, h1 = tl.associative_scan((a, b), 0, _affine_op, reverse=REVERSE)
+    tl.store(out_a + tl.arange(0, 512), h0)
+    tl.store(out_b + tl.arange(0, 512), h1)
+
+
+@pytest.mark.parametrize("reverse", [False, True])
+def test_scan_of_an_interleaved_view(reverse):
+    _say(f"scan of a transposed view reverse={reverse}")
+    rng = np.random.default_rng(7)
+    a = rng.integers(-3, 4, (2, 256)).astype(np.int32)
+    b = rng.integers(-100, 100, (2, 256)).astype(np.int32)
+    oa, ob = np.empty(512, np.int32), np.empty(512, np.int32)
+    _view_scan_kernel[(1,)](a, b, oa, ob, REVERSE=reverse)
+    with np.errstate(over="ignore"):
+        wa, wb = _affine_ref(a.T.reshape(-1), b.T.reshape(-1), 0, reverse)
+    np.testing.assert_array_equal(oa, wa)
+    np.testing.assert_array_equal(ob, wb)
