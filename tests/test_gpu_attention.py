@@ -105,3 +105,29 @@ def test_accumulator_row_reduction(dot_warps):
     _dot_row_max[(1,)](a, b, out, m, n, k, BM=64, BN=32, BK=16, dot_warps=dot_warps)
     np.testing.assert_allclose(out, (a.astype(np.float32) @ b.astype(np.float32)).max(1),
                                atol=1e-4)
+
+
+# -- matmul shapes (reference: tests/test_interpreter.py:73-88, 730-770) ------------------
+
+SHAPES = [(64, 64, 64), (513, 513, 513), (1000, 300, 777), (2048, 2048, 2048)]
+
+
+@pytest.mark.parametrize("variant", ["desc", "pointer"])
+@pytest.mark.parametrize("mkn", SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
+def test_matmul_shapes(dtype, mkn, variant):
+    import torch
+    from examples.matmul import matmul, matmul_desc
+    print(f"[case] matmul {variant} {mkn} {dtype}", flush=True)
+    m, k, n = mkn
+    g = torch.Generator().manual_seed(m + k + n)
+    td = getattr(torch, dtype)
+    a = torch.randn(m, k, generator=g).to(td).cuda()
+    b = torch.randn(k, n, generator=g).to(td).cuda()
+    c = (matmul_desc if variant == "desc" else matmul)(a, b)
+    torch.cuda.synchronize()
+    want = a.double().cpu() @ b.double().cpu()
+    # fp32 operands go through MFMA in fp32; half outputs round once to their type
+    tol = {"float32": 1e-4 * k ** 0.5, "float16": 2e-3 * k ** 0.5 / 8,
+           "bfloat16": 1.6e-2 * k ** 0.5 / 8}[dtype]
+    torch.testing.assert_close(c.double().cpu(), want, atol=tol, rtol=tol)
