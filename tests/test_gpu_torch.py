@@ -246,3 +246,28 @@ def test_math_is_bit_identical_across_launch_paths(example):
     outs.append(eo.numpy())
     assert outs[0].view(np.uint32).tolist() == outs[1].view(np.uint32).tolist()
     assert outs[0].view(np.uint32).tolist() == outs[2].view(np.uint32).tolist()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("pad", [0, 3, 64])
+@pytest.mark.parametrize("case", ["softmax", "rmsnorm"])
+def test_examples_on_padded_framework_arrays(case, pad):
+    # row views into wider allocations: the row stride is the allocation's, not the width
+    # (reference test strategy: tests/test_interop.py test_examples_on_framework_arrays)
+    import torch
+    print(f"[case] padded {case} pad={pad}", flush=True)
+    m, n = 24, 1000
+    g = torch.Generator().manual_seed(pad)
+    base = torch.randn(m, n + pad, generator=g).cuda()
+    x = base[:, :n]
+    if case == "softmax":
+        from examples.softmax import softmax
+        got = softmax(x)
+        want = R.softmax(x.cpu().numpy())
+    else:
+        from examples.rmsnorm import rmsnorm
+        w = (torch.rand(n, generator=g) + 0.5).cuda()
+        got = rmsnorm(x, w)
+        want = R.rmsnorm(x.cpu().numpy(), w.cpu().numpy())
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(got.cpu().numpy(), want, rtol=1e-5, atol=1e-6)
