@@ -4,13 +4,26 @@ Prints one JSON line (the driver's contract). The headline workload is BASELINE 
 (`configs[1]`): row softmax over fp32 [4096, 8192]; `value` is its whole-job GB/s with
 inputs resident in HBM. The same run measures every other config (vector add 2^28,
 RMSNorm, fp16 4096^3 matmul and + bias + GELU, bf16 flash attention causal 4096 and
-non-causal 1024, int32 histogram and cumsum) and reports them under "workloads", each with
-its roofline fraction. Kernel times come from HIP events recorded on the launch stream
-around the timed launches; inputs rotate over several buffer sets totalling > 512 MB so
-the 256 MB Infinity Cache can't serve them.
+non-causal 1024, int32 histogram and cumsum) and reports each under "workloads" with its
+roofline fraction.
+
+Every launch timed here comes from `examples/workloads.py`, the table that
+`tests/test_gpu_bench_configs.py` checks variant by variant at the same full sizes against
+the CPU oracle. Matmul and attention take the variant the library's autotuner picks
+(`matmul_desc_tuned`, `matmul_bias_gelu_tuned`, `attention_tuned_kernel` over
+`enceladus.configs`); the HBM-bound rows time each listed `num_warps` and report the
+fastest. Kernel times come from HIP events recorded on the launch stream (torch's current
+stream) around K pre-packed launches after W warm-ups; inputs of the HBM-bound rows rotate
+over buffer sets totalling > 600 MB so the 256 MB Infinity Cache cannot serve them.
+
+The CPU baseline (`cpu_baseline`, and `cpu` under each workload) times the oracle
+interpreter (a restatement of the reference's `ENCELADUS_INTERPRET=1` interpreter, one
+core) on a random sample of each grid's programs, and NumPy's closed form (the examples'
+`reference()` functions) on a bounded slice, both extrapolated to the full workload.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME[,NAME]]
                        [--no-cpu-baseline]
+NAME is a workload of examples/workloads.py, or copy_calib (the counter calibration copy).
 """
 
 from __future__ import annotations
@@ -19,6 +32,7 @@ import argparse
 import json
 import math
 import os
+import platform
 import sys
 import time
 
@@ -28,7 +42,7 @@ os.environ.setdefault("ENCELADUS_CACHE_DIR", os.path.join(ROOT, ".ek_cache"))
 
 HBM_PEAK = 8.0e12          # bytes/s (MI355X HBM3E)
 MFMA_PEAK_F16 = 2.5e15     # dense fp16/bf16 FLOP/s
-GIB = 1 << 30
+METRIC = "matmul/flash-attn TFLOP/s, softmax GB/s, % of MI355X roofline"
 
 
 def log(msg):
@@ -55,16 +69,24 @@ class Timer:
         return s.elapsed_time(e) / steps  # ms per launch
 
 
-def make_launch(jfn, grid, args, num_warps=4, dot_warps=None, **constexprs):
+def make_launch(jfn, grid, args, options):
+    """A pre-packed launch of `jfn[grid](*args, **options)` on torch's current stream: the
+    same specialization lookup as the Python front door, with no Python in the timed loop
+    beyond one ctypes call per dispatch."""
     import ctypes
+
+    import torch
+
     from enceladus_amd.runtime import hip
-    vals = jfn._bind(args, constexprs)
-    lc = jfn._lookup(vals, num_warps, dot_warps)
+    options = dict(options)
+    nw = options.pop("num_warps", 4)
+    dw = options.pop("dot_warps", None)
+    vals = jfn._bind(args, options)
+    lc = jfn._lookup(vals, nw, dw)
     packed = []
     for n in lc.runtime_names:
         v = vals[n]
         packed.append(v.data_ptr() if hasattr(v, "data_ptr") else v)
-    import torch
     sid = int(torch.cuda.current_stream().cuda_stream)
     # the kernel's dispatches (a privatised histogram adds its second flush level)
     disp = lc.ck.prepare(grid, lc.ck.pack(packed), sid)
@@ -81,266 +103,276 @@ def make_launch(jfn, grid, args, num_warps=4, dot_warps=None, **constexprs):
     return launch
 
 
-# (BM, BN, BK, num_warps) swept for the matmul rows: the autotuner's MI355X candidates
-MATMUL_CONFIGS = [(256, 256, 64, 4), (256, 256, 32, 4), (256, 128, 64, 4), (128, 256, 64, 4),
-                  (128, 128, 64, 4), (256, 256, 64, 8), (256, 256, 32, 8)]
+def rotation_sets(torch, wl, base):
+    """Extra input sets (rolled copies of the seeded inputs) so that the sets together
+    exceed 600 MB: consecutive launches then read HBM, not the Infinity Cache."""
+    sets = [base]
+    n = max(2, math.ceil(600e6 / wl.work)) if wl.bound == "hbm" else 1
+    for i in range(1, n):
+        s = {}
+        for k, t in base.items():
+            s[k] = torch.empty_like(t) if k in wl.outputs else torch.roll(t, i, 0)
+        sets.append(s)
+    return sets
 
 
-# (BLOCK_M, BLOCK_N, num_warps) swept for the attention rows (dot_warps = (num_warps, 1))
-ATTN_CONFIGS = [(128, 64, 4), (128, 128, 4), (128, 32, 4), (256, 64, 8), (256, 128, 8)]
+def measure(torch, timer, wl, steps, warmup):
+    from examples import workloads as W
+    host = wl.inputs()
+    base = W.device_buffers(wl, host)
+    sets = rotation_sets(torch, wl, base)
+    r = {"name": wl.name, "bound": wl.bound, "dtype": wl.dtype, "tested_by":
+         "tests/test_gpu_bench_configs.py"}
+    if wl.tuned is not None:
+        # the library's autotuner picks the variant (on the seeded inputs)
+        tuned = wl.tuned()
+        _, args = wl.args(base, wl.variants[0])
 
-
-# num_warps swept for the HBM-bound row kernels (a launch option, as the autotuner would)
-HBM_WARPS = (4, 8, 16)
-
-
-def best_of(timer, steps, warmup, options, build):
+        def grid(meta):
+            return wl.args(base, W.Variant(tuple(meta.items())))[0]
+        t0 = time.perf_counter()
+        tuned[grid](*args, **wl.fixed)
+        torch.cuda.synchronize()
+        cfg = tuned.config_for(*args, **wl.fixed)
+        v = wl.variant_of(cfg)
+        key = tuned._key(tuned_named(tuned, args, wl.fixed))
+        for c, ms in sorted(tuned.timings.get(key, {}).items(), key=lambda x: x[1]):
+            log(f"    autotune {c}: {ms * 1e3:.1f} us")
+        log(f"    autotuner picked {v.label} ({time.perf_counter() - t0:.1f} s)")
+        assert v in wl.variants, f"autotuner pick {v} is not in the tested table"
+        r["selected_by"] = "autotuner"
+        choices = [v]
+    else:
+        r["selected_by"] = "fastest listed variant"
+        choices = wl.variants
     best = None
-    for o in options:
-        ls = build(o)
-        ms = timer.run(ls, steps, warmup)
-        log(f"    num_warps={o}: {ms * 1e3:.1f} us")
+    for v in choices:
+        launches = [make_launch(wl.kernel(), *wl.args(s, v), v.options()) for s in sets]
+        k = steps if wl.bound == "hbm" else max(5, steps // 2)
+        if wl.name == "vector_add" or wl.name.startswith("attention"):
+            k = max(4, steps // 4)
+        ms = timer.run(launches, k, max(2, warmup // 2))
+        log(f"    {v.label}: {ms * 1e3:.1f} us")
         if best is None or ms < best[0]:
-            best = (ms, ls, o)
-    return best
+            best = (ms, v, launches[0].ck.name)
+    ms, v, kname = best
+    r.update({"config": f"{wl.describe} {v.label}", "variant": v.label, "ms": ms,
+              "kernel": kname})
+    if wl.bound == "hbm":
+        r["bytes"] = wl.work
+        r["gbps"] = wl.work / ms / 1e6
+        r["roofline_frac"] = r["gbps"] * 1e9 / HBM_PEAK
+    else:
+        r["flop"] = wl.work
+        r["tflops"] = wl.work / ms / 1e9
+        r["roofline_frac"] = r["tflops"] * 1e12 / MFMA_PEAK_F16
+    r["traffic"] = measured_traffic(wl.name)
+    del sets, base
+    return r, host
 
 
-def sets_for(bytes_per_set):
-    return max(2, math.ceil(600e6 / bytes_per_set))
-
-
-# ------------------------------------------------------------------------- workloads
-
-def w_softmax(torch, timer, steps, warmup):
-    from examples.softmax import softmax_kernel
-    M, N = 4096, 8192
-    nbytes = M * N * 4 * 2
-    k = sets_for(nbytes)
-    xs = [torch.randn(M, N, device="cuda", generator=None) for _ in range(k)]
-    outs = [torch.empty_like(x) for x in xs]
-    ms, launches, nw = best_of(timer, steps, warmup, HBM_WARPS, lambda nw: [
-        make_launch(softmax_kernel, (M,), (o, x, N, N, N), BLOCK=8192, num_warps=nw)
-        for x, o in zip(xs, outs)])
-    return {"name": "softmax", "config": f"fp32 [4096, 8192] num_warps={nw}", "ms": ms,
-            "bytes": nbytes, "gbps": nbytes / ms / 1e6, "dtype": "fp32", "bound": "hbm",
-            "kernel": launches[0].ck.name}
-
-
-def w_rmsnorm(torch, timer, steps, warmup):
-    from examples.rmsnorm import rmsnorm_kernel
-    M, N = 4096, 8192
-    nbytes = M * N * 4 * 2 + N * 4
-    k = sets_for(nbytes)
-    g = torch.Generator(device="cpu").manual_seed(1)
-    w = (torch.rand(N, generator=g) + 0.5).cuda()
-    xs = [torch.randn(M, N, device="cuda") for _ in range(k)]
-    outs = [torch.empty_like(x) for x in xs]
-    ms, launches, nw = best_of(timer, steps, warmup, HBM_WARPS, lambda nw: [
-        make_launch(rmsnorm_kernel, (M,), (x, w, o, N, N, N, 1e-6), BLOCK=8192, num_warps=nw)
-        for x, o in zip(xs, outs)])
-    return {"name": "rmsnorm", "config": f"fp32 [4096, 8192] eps 1e-6 num_warps={nw}", "ms": ms,
-            "bytes": nbytes, "gbps": nbytes / ms / 1e6, "dtype": "fp32", "bound": "hbm",
-            "kernel": launches[0].ck.name}
-
-
-def w_vector_add(torch, timer, steps, warmup):
-    from examples.vector_add import add_kernel
-    n = 1 << 28
-    nbytes = 12 * n
-    xs = [torch.randn(n, device="cuda") for _ in range(2)]
-    y = torch.ones(n, device="cuda")
-    out = torch.empty(n, device="cuda")
-    launches = [make_launch(add_kernel, (n // 1024,), (x, y, out, n), BLOCK=1024) for x in xs]
-    ms = timer.run(launches, max(4, steps // 4), max(2, warmup // 4))
-    return {"name": "vector_add", "config": "fp32 n=2^28 BLOCK 1024", "ms": ms,
-            "bytes": nbytes, "gbps": nbytes / ms / 1e6, "dtype": "fp32", "bound": "hbm",
-            "kernel": launches[0].ck.name}
-
-
-def w_matmul(torch, timer, steps, warmup, fused=False):
-    from examples.matmul import matmul_desc_kernel
-    from examples.matmul_fused import matmul_bias_gelu_kernel
-    M = N = K = 4096
-    g = torch.Generator(device="cpu").manual_seed(0)
-    a = (torch.randn(M, K, generator=g) / 64).half().cuda()
-    b = (torch.randn(K, N, generator=g) / 64).half().cuda()
-    bias = torch.randn(N, generator=g).half().cuda()
-    c = torch.empty(M, N, dtype=torch.float16, device="cuda")
-    best = None
-    for bm, bn, bk, nw in MATMUL_CONFIGS:
-        cfg = dict(BM=bm, BN=bn, BK=bk, num_warps=nw)
-        grid = (N // bn, M // bm)
-        if fused:
-            l = make_launch(matmul_bias_gelu_kernel, grid, (a, b, bias, c, M, N, K, K, N, N), **cfg)
-        else:
-            l = make_launch(matmul_desc_kernel, grid, (a, b, c, M, N, K, K, N, N), **cfg)
-        ms = timer.run([l], max(5, steps // 2), max(2, warmup // 2))
-        log(f"    BM={bm} BN={bn} BK={bk} warps={nw}: {ms * 1e3:.1f} us")
-        if best is None or ms < best[0]:
-            best = (ms, l, cfg)
-    ms, l, cfg = best
-    flop = 2 * M * N * K
-    return {"name": "matmul_gelu" if fused else "matmul", "config": "fp16 4096^3 fp32 acc"
-            + (" + bias + GELU" if fused else "") + f" {cfg}", "ms": ms, "flop": flop,
-            "tflops": flop / ms / 1e9, "dtype": "fp16", "bound": "mfma", "kernel": l.ck.name}
-
-
-def w_attention(torch, timer, steps, warmup, causal=True, n=4096):
-    from examples.flash_attention import attention_kernel
-    B, H, D = 4, 32, 128
-    g = torch.Generator(device="cpu").manual_seed(0)
-    q, k, v = (torch.randn(B, H, n, D, generator=g).bfloat16().cuda() for _ in range(3))
-    o = torch.empty_like(q)
-    best = None
-    for bm, bn, nw in ATTN_CONFIGS:
-        l = make_launch(attention_kernel, (n // bm, B * H), (q, k, v, o, D ** -0.5, n, n * D, D),
-                        HEAD_DIM=D, BLOCK_M=bm, BLOCK_N=bn, CAUSAL=causal, num_warps=nw,
-                        dot_warps=(nw, 1))
-        ms = timer.run([l], max(3, steps // 4), max(1, warmup // 4))
-        log(f"    BLOCK_M={bm} BLOCK_N={bn} warps={nw}: {ms * 1e3:.1f} us")
-        if best is None or ms < best[0]:
-            best = (ms, l, (bm, bn, nw))
-    ms, l, cfg = best
-    flop = 4 * B * H * n * n * D // (2 if causal else 1)
-    return {"name": f"attention_{'causal' if causal else 'noncausal'}_{n}",
-            "config": f"bf16 [4,32,{n},128] {'causal' if causal else 'non-causal'} "
-                      f"BLOCK_M/N/warps={cfg}", "ms": ms,
-            "flop": flop, "tflops": flop / ms / 1e9, "dtype": "bf16", "bound": "mfma", "kernel": l.ck.name}
-
-
-def w_histogram(torch, timer, steps, warmup):
-    from examples.histogram import histogram_kernel
-    n = 1 << 26
-    g = torch.Generator(device="cpu").manual_seed(0)
-    xs = [torch.randint(0, 1024, (n,), generator=g, dtype=torch.int32).cuda() for _ in range(3)]
-    h = torch.zeros(1024, dtype=torch.int32, device="cuda")
-    ms, launches, nw = best_of(timer, max(4, steps // 4), 2, (4, 8), lambda nw: [
-        make_launch(histogram_kernel, (n // 1024,), (x, h, n, 0.0, 1.0), NUM_BINS=1024,
-                    BLOCK=1024, num_warps=nw) for x in xs])
-    nbytes = 4 * n
-    return {"name": "histogram", "config": f"int32 2^26 -> 1024 bins num_warps={nw}", "ms": ms,
-            "bytes": nbytes,
-            "gbps": nbytes / ms / 1e6, "dtype": "int32", "bound": "hbm", "kernel": launches[0].ck.name}
-
-
-def w_cumsum(torch, timer, steps, warmup):
-    from examples.cumsum import cumsum_kernel
-    M, N = 8192, 4096
-    nbytes = M * N * 4 * 2
-    g = torch.Generator(device="cpu").manual_seed(0)
-    xs = [torch.randint(-100, 100, (M, N), generator=g, dtype=torch.int32).cuda()
-          for _ in range(sets_for(nbytes))]
-    outs = [torch.empty_like(x) for x in xs]
-    ms, launches, nw = best_of(timer, steps, warmup, HBM_WARPS, lambda nw: [
-        make_launch(cumsum_kernel, (M,), (o, x, M, N, N, N), REVERSE=False, BLOCK_M=1,
-                    BLOCK_N=4096, num_warps=nw) for x, o in zip(xs, outs)])
-    return {"name": "cumsum", "config": f"int32 [8192, 4096] rows num_warps={nw}", "ms": ms,
-            "bytes": nbytes,
-            "gbps": nbytes / ms / 1e6, "dtype": "int32", "bound": "hbm", "kernel": launches[0].ck.name}
-
-
-def w_torch_matmul(torch, timer, steps, warmup):
-    """Calibration only: torch.matmul (hipBLASLt) on the same fp16 4096^3 problem."""
-    M = N = K = 4096
-    a = (torch.randn(M, K, device="cuda") / 64).half()
-    b = (torch.randn(K, N, device="cuda") / 64).half()
-    c = torch.empty(M, N, dtype=torch.float16, device="cuda")
-    ms = timer.run([lambda: torch.matmul(a, b, out=c)], max(5, steps // 2), 3)
-    flop = 2 * M * N * K
-    return {"name": "torch_matmul", "config": "hipBLASLt fp16 4096^3 (calibration, not ours)",
-            "ms": ms, "flop": flop, "tflops": flop / ms / 1e9, "dtype": "fp16", "bound": "mfma",
-            "kernel": "torch.matmul"}
-
-
-def w_torch_attention(torch, timer, steps, warmup, causal=True, n=4096):
-    """Calibration only: torch's scaled_dot_product_attention (its ROCm flash kernel) on
-    the same bf16 [4, 32, n, 128] problem."""
-    import torch.nn.functional as F
-    B, H, D = 4, 32, 128
-    q, k, v = (torch.randn(B, H, n, D, device="cuda").bfloat16() for _ in range(3))
-    ms = timer.run([lambda: F.scaled_dot_product_attention(q, k, v, is_causal=causal)],
-                   max(3, steps // 4), 2)
-    flop = 4 * B * H * n * n * D // (2 if causal else 1)
-    return {"name": "torch_attention", "config": f"torch SDPA bf16 [4,32,{n},128] "
-            f"{'causal' if causal else 'non-causal'} (calibration, not ours)", "ms": ms,
-            "flop": flop, "tflops": flop / ms / 1e9, "dtype": "bf16", "bound": "mfma",
-            "kernel": "torch.sdpa"}
-
-
-def w_copy_calib(torch, timer, steps, warmup):
-    """Calibration for HBM counters: a plain 256 MiB device-to-device copy."""
+def copy_calibration(torch, timer, steps):
+    """A plain 256 MiB device-to-device copy (torch's copy kernel): the known-size kernel
+    that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes. Run only when named
+    in --only."""
     n = 64 << 20
     x = torch.randn(n, device="cuda")
     y = torch.empty_like(x)
     ms = timer.run([lambda: y.copy_(x)], max(4, steps // 4), 2)
-    nbytes = 8 * n
     return {"name": "copy_calib", "config": "torch copy 256 MiB -> 256 MiB", "ms": ms,
-            "bytes": nbytes, "gbps": nbytes / ms / 1e6, "dtype": "fp32", "bound": "hbm", "kernel": "copy"}
+            "bytes": 8 * n, "gbps": 8 * n / ms / 1e6, "bound": "hbm", "dtype": "fp32",
+            "kernel": "copy", "roofline_frac": 8 * n / ms / 1e6 * 1e9 / HBM_PEAK}
 
 
-WORKLOADS = {
-    "softmax": w_softmax, "rmsnorm": w_rmsnorm, "vector_add": w_vector_add,
-    "matmul": lambda t, tm, s, w: w_matmul(t, tm, s, w, False),
-    "matmul_gelu": lambda t, tm, s, w: w_matmul(t, tm, s, w, True),
-    "attention_causal": lambda t, tm, s, w: w_attention(t, tm, s, w, True, 4096),
-    "attention_noncausal": lambda t, tm, s, w: w_attention(t, tm, s, w, False, 1024),
-    "histogram": w_histogram, "cumsum": w_cumsum,
-    "torch_matmul": w_torch_matmul,
-    "torch_attention": w_torch_attention,
-    "copy_calib": w_copy_calib,
-}
-DEFAULT = [k for k in WORKLOADS if k not in ("torch_matmul", "torch_attention", "copy_calib")]
+def tuned_named(tuned, args, fixed):
+    from enceladus_amd.runtime.autotuner import _named
+    return _named(tuned.fn, args, fixed)
 
 
-def measured_traffic(kernel: str):
-    """HBM bytes per launch for `kernel` from the committed rocprofv3 counter summary."""
+def measured_traffic(name: str):
+    """HBM bytes per launch of workload `name` from the committed rocprofv3 counter
+    summaries (`traffic_bytes_per_launch[name]: N` lines), or None."""
     import glob
-    for path in glob.glob(os.path.join(ROOT, "profiles", "*_hbm_counters.txt")):
-        text = open(path).read()
-        if kernel in text:
-            for line in text.splitlines():
-                if line.startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":")[1])
+    tag = f"traffic_bytes_per_launch[{name}]:"
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*counters*.txt"))):
+        for line in open(path).read().splitlines():
+            if line.startswith(tag):
+                return int(line.split(":")[1])
     return None
 
 
-def cpu_baseline(budget_s=12.0):
-    """The oracle interpreter (1 core) on a bounded sample of softmax rows."""
-    import numpy as np
-    from examples.softmax import softmax_kernel
-    from oracle import interpreter as O
-    M, N = 4096, 8192
-    x = np.random.default_rng(0).standard_normal((M, N), dtype=np.float32)
-    out = np.empty_like(x)
-    rows = 0
-    t0 = time.perf_counter()
-    order = np.random.default_rng(1).permutation(M)
-    while time.perf_counter() - t0 < budget_s and rows < M:
-        O.run_grid(softmax_kernel, (M,), out, x, N, N, N, BLOCK=8192,
-                   programs=[(int(order[rows]),)])
-        rows += 1
-    dt = time.perf_counter() - t0
-    gbps = rows * N * 4 * 2 / dt / 1e9
-    return {"value": gbps, "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{rows} random rows of the fp32 [4096, 8192] softmax through the "
-                      f"oracle interpreter in {dt:.1f} s (programs are independent)"}
+# ------------------------------------------------------------------------- CPU baseline
 
+def host_info():
+    model = platform.processor() or ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except AttributeError:
+        aff = os.cpu_count()
+    blas = None
+    try:
+        from threadpoolctl import threadpool_info
+        blas = [{"api": d.get("internal_api"), "threads": d.get("num_threads")}
+                for d in threadpool_info()]
+    except Exception:  # noqa: BLE001
+        pass
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count(), "affinity": aff,
+            "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS"),
+            "OPENBLAS_NUM_THREADS": os.environ.get("OPENBLAS_NUM_THREADS"), "blas": blas}
+
+
+def _sample_programs(grid, budget_s, run_one, seed=1, stratify=None):
+    """Runs a random sample of program ids through `run_one(pid)` for about `budget_s`;
+    returns (programs run, seconds). `stratify(pid)` orders causal programs so that the
+    sample covers every row of blocks evenly."""
+    import numpy as np
+    total = 1
+    for g in grid:
+        total *= g
+    order = np.random.default_rng(seed).permutation(total)
+    if stratify is not None:
+        order = sorted(order.tolist(), key=stratify)
+    done = 0
+    t0 = time.perf_counter()
+    while done < total and (done == 0 or time.perf_counter() - t0 < budget_s):
+        i = int(order[done])
+        pid = (i % grid[0], (i // grid[0]) % (grid[1] if len(grid) > 1 else 1))
+        run_one(pid)
+        done += 1
+    return done, time.perf_counter() - t0, total
+
+
+def cpu_workload(wl, host, v, budget_s=1.5):
+    """The oracle interpreter on sampled programs and NumPy's closed form on a slice of
+    workload `wl` (inputs `host`, variant `v`), both scaled to the full workload."""
+    import numpy as np
+
+    from examples import workloads as W
+    from oracle import interpreter as O
+    from oracle import reference_np as R
+    c = dict(v.constexprs)
+    out = {}
+    if wl.name in ("softmax", "rmsnorm", "cumsum"):
+        x = host["x"]
+        m, n = x.shape
+        y = np.zeros_like(x)
+        if wl.name == "softmax":
+            def one(pid):
+                O.run_grid(wl.kernel(), (m,), y, x, n, n, n, **c, programs=[pid])
+        elif wl.name == "rmsnorm":
+            def one(pid):
+                O.run_grid(wl.kernel(), (m,), x, host["w"], y, n, n, n, 1e-6, **c,
+                           programs=[pid])
+        else:
+            def one(pid):
+                O.run_grid(wl.kernel(), (m,), y, x, m, n, n, n, **c, programs=[pid])
+        grid = (m,)
+        rows = 512
+        t0 = time.perf_counter()
+        if wl.name == "softmax":
+            R.softmax(x[:rows])
+        elif wl.name == "rmsnorm":
+            R.rmsnorm(x[:rows], host["w"])
+        else:
+            R.cumsum(x[:rows])
+        np_s = (time.perf_counter() - t0) * m / rows
+        np_sample = f"closed form on {rows} of {m} rows"
+    elif wl.name == "vector_add":
+        x, yv = host["x"], host["y"]
+        n = x.size
+        o = np.zeros(n, np.float32)
+
+        def one(pid):
+            O.run_grid(wl.kernel(), (n // 1024,), x, yv, o, n, BLOCK=1024, programs=[pid])
+        grid = (n // 1024,)
+        k = 1 << 24
+        t0 = time.perf_counter()
+        R.vector_add(x[:k], yv[:k])
+        np_s = (time.perf_counter() - t0) * n / k
+        np_sample = f"closed form on 2^24 of {n} elements"
+    elif wl.name == "histogram":
+        x = host["x"]
+        n = x.size
+        hist = np.zeros(W.HIST_BINS, np.int32)
+
+        def one(pid):
+            O.run_grid(wl.kernel(), (n // 1024,), x, hist, n, 0.0, 1.0, **c, programs=[pid])
+        grid = (n // 1024,)
+        t0 = time.perf_counter()
+        R.histogram(x, W.HIST_BINS, 0.0, 1024.0)
+        np_s = time.perf_counter() - t0
+        np_sample = "closed form (np.bincount) on all elements"
+    elif wl.name.startswith("matmul"):
+        a, b = host["a"], host["b"]
+        mm = a.shape[0]
+        cc = np.zeros((mm, mm), np.float16)
+        grid = (mm // c["BN"], mm // c["BM"])
+        if wl.name == "matmul":
+            def one(pid):
+                O.run_grid(wl.kernel(), grid, a, b, cc, mm, mm, mm, mm, mm, mm, **c,
+                           programs=[pid])
+        else:
+            def one(pid):
+                O.run_grid(wl.kernel(), grid, a, b, host["bias"], cc, mm, mm, mm, mm, mm, mm,
+                           **c, programs=[pid])
+        rows = 256
+        t0 = time.perf_counter()
+        if wl.name == "matmul":
+            R.matmul(a[:rows], b)
+        else:
+            R.matmul_bias_gelu(a[:rows], b, host["bias"])
+        np_s = (time.perf_counter() - t0) * mm / rows
+        np_sample = f"closed form on {rows} of {mm} rows of A"
+    else:   # attention
+        import torch
+        q, k, vv = host["q"], host["k"], host["v"]
+        z, h, n, d = q.shape
+        ob = torch.zeros_like(q)
+        bm = c["BLOCK_M"]
+        grid = (n // bm, z * h)
+
+        def one(pid):
+            O.run_grid(wl.kernel(), grid, q, k, vv, ob, d ** -0.5, n, n * d, d, **c,
+                       programs=[pid])
+        t0 = time.perf_counter()
+        R.attention(q[:1, :1].float().numpy(), k[:1, :1].float().numpy(),
+                    vv[:1, :1].float().numpy(), c["CAUSAL"])
+        np_s = (time.perf_counter() - t0) * z * h
+        np_sample = f"float64 closed form on 1 of {z * h} (batch, head) slices"
+    strat = None
+    if wl.name == "attention_causal":
+        def strat(i):   # interleave start_m blocks so a short sample spans all of them
+            return (i // grid[0], i % grid[0])
+    done, secs, total = _sample_programs(grid, budget_s, one, stratify=strat)
+    interp_s = secs * total / done
+    unit = "GB/s" if wl.bound == "hbm" else "TFLOP/s"
+    scale = 1e9 if wl.bound == "hbm" else 1e12
+    out["interpreter"] = {"value": wl.work / interp_s / scale, "unit": unit, "cores": 1,
+                          "kind": "port", "full_run_s_est": interp_s,
+                          "sample": f"{done} of {total} programs in {secs:.2f} s"}
+    out["numpy"] = {"value": wl.work / np_s / scale, "unit": unit, "kind": "numpy",
+                    "full_run_s_est": np_s, "sample": np_sample}
+    return out
+
+
+# ----------------------------------------------------------------------------- main
 
 def main():
+    from examples import workloads as W
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=40)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default="")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--mm", default="", help="only this matmul config: BM,BN,BK,num_warps")
-    ap.add_argument("--attn", default="", help="only this attention config: BM,BN,num_warps")
     args = ap.parse_args()
-    global MATMUL_CONFIGS, ATTN_CONFIGS
-    if args.mm:
-        MATMUL_CONFIGS = [tuple(int(x) for x in args.mm.split(","))]
-    if args.attn:
-        ATTN_CONFIGS = [tuple(int(x) for x in args.attn.split(","))]
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; multi-GPU runs are out "
                           "of scope (every config shards with no exchange between GPUs)"}))
@@ -351,22 +383,34 @@ def main():
     info = hip.device_info(0)
     log(f"device: {info.name.decode()} {info.arch.decode()} CUs={info.compute_units}")
     timer = Timer(torch)
-    names = args.only.split(",") if args.only else DEFAULT
+    table = W.table()
+    names = args.only.split(",") if args.only else list(table)
     results = {}
+    cpu = {}
     for n in names:
         log(f"[bench] {n} ...")
-        r = WORKLOADS[n](torch, timer, args.steps, args.warmup)
-        if r["bound"] == "hbm":
-            r["roofline_frac"] = r["gbps"] * 1e9 / HBM_PEAK
-        else:
-            r["roofline_frac"] = r["tflops"] * 1e12 / MFMA_PEAK_F16
+        if n == "copy_calib":
+            results[n] = copy_calibration(torch, timer, args.steps)
+            log(f"[bench] copy_calib: {results[n]['gbps']:.0f} GB/s")
+            continue
+        r, host = measure(torch, timer, table[n], args.steps, args.warmup)
         results[n] = r
         log(f"[bench] {n}: {r['ms'] * 1e3:.1f} us  " +
             (f"{r['gbps']:.0f} GB/s" if "gbps" in r else f"{r['tflops']:.1f} TFLOP/s") +
             f"  ({100 * r['roofline_frac']:.1f}% of roofline)")
-    head = results.get("softmax") or next(iter(results.values()))
+        if not args.no_cpu_baseline:
+            v = next(x for x in table[n].variants if x.label == r["variant"])
+            cpu[n] = cpu_workload(table[n], host, v)
+            r["cpu"] = cpu[n]
+            log(f"    cpu: interpreter {cpu[n]['interpreter']['value']:.4g} "
+                f"{cpu[n]['interpreter']['unit']} ({cpu[n]['interpreter']['sample']}), "
+                f"numpy {cpu[n]['numpy']['value']:.4g}")
+        del host
+        torch.cuda.empty_cache()
+    real = {k: r for k, r in results.items() if k != "copy_calib"} or results
+    head = real.get("softmax") or next(iter(real.values()))
     line = {
-        "metric": "matmul/flash-attn TFLOP/s, softmax GB/s, % of MI355X roofline",
+        "metric": METRIC,
         "value": round(head.get("gbps", head.get("tflops", 0.0)), 2),
         "unit": "GB/s" if "gbps" in head else "TFLOP/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -380,13 +424,17 @@ def main():
                      {"bound": "mfma", "achieved": round(head["tflops"], 1),
                       "peak": MFMA_PEAK_F16 / 1e12, "unit": "TFLOP/s"}) | {
                      "frac": round(head["roofline_frac"], 4),
-                     "traffic": measured_traffic(head["kernel"])},
+                     "traffic": head.get("traffic")},
         "workloads": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
                           for kk, vv in v.items()} for k, v in results.items()},
     }
-    if not args.no_cpu_baseline:
-        log("[bench] cpu baseline (oracle interpreter, bounded sample) ...")
-        line["cpu_baseline"] = cpu_baseline()
+    if cpu:
+        hc = cpu.get(head["name"]) or next(iter(cpu.values()))
+        ib = hc["interpreter"]
+        line["cpu_baseline"] = {"value": ib["value"], "unit": ib["unit"], "cores": 1,
+                                "kind": "port", "sample": f"{head['name']}: oracle "
+                                f"interpreter, {ib['sample']}, scaled to the full workload",
+                                "host": host_info()}
     print(json.dumps(line), flush=True)
 
 

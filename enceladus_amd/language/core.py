@@ -3,7 +3,9 @@
 The dtype table mirrors the reference language's twelve types
 (reference: src/enceladus/language/core.py:45-117). NumPy has no bfloat16 without
 `ml_dtypes`, so host-side bfloat16 arrays are carried as `uint16` bit patterns (or as
-torch tensors); `dtype.to_numpy()` reports `uint16` storage for `bfloat16`.
+torch tensors); `dtype.to_numpy()` reports `uint16` storage for `bfloat16`, and
+`BF16_TAG` (a 2-byte void dtype of kind "V", the kind ml_dtypes' bfloat16 reports) is the
+NumPy-side name of the element type (`enceladus.element_dtype`).
 """
 
 from __future__ import annotations
@@ -96,6 +98,8 @@ _NUMPY = {
     "fp16": np.dtype(np.float16), "bf16": np.dtype(np.uint16), "fp32": np.dtype(np.float32),
 }
 _FROM_NUMPY = {v: k for k, v in _NUMPY.items() if k != "bf16"}
+# The NumPy-side name of bfloat16 (kind "V", itemsize 2, tagged by its metadata).
+BF16_TAG = np.dtype("V2", metadata={"enceladus_dtype": "bfloat16"})
 _BY_NAME: dict[str, dtype] = {}
 for _d in ALL_DTYPES:
     _BY_NAME[_d.name] = _d
@@ -106,7 +110,9 @@ _BY_NAME["bool"] = int1
 
 def dtype_from_numpy(np_dtype: Any) -> dtype:
     d = np.dtype(np_dtype)
-    name = _FROM_NUMPY.get(d)
+    if (d.metadata or {}).get("enceladus_dtype") == "bfloat16":
+        return bfloat16
+    name = _FROM_NUMPY.get(d) if d.kind != "V" else None
     if name is not None:
         return _BY_NAME[name]
     if d == np.float64:

@@ -342,7 +342,8 @@ class JITFunction:
         # no_staging, no_gemm_template, coarsen); part of the specialization key below.
         for item in filter(None, os.environ.get("ENCELADUS_CODEGEN", "").split(",")):
             k, _, v = item.partition("=")
-            options[k.strip()] = int(v) if v.strip().isdigit() else True
+            v = v.strip()
+            options[k.strip()] = int(v) if v.isdigit() else (v if v else True)
         # ENCELADUS_DEBUG=1 keeps tl.device_assert checks (part of the key below)
         options["debug"] = _debug()
         fn_ir = C.build_module(self, types, facts, consts, num_warps, options)

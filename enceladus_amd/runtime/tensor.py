@@ -310,12 +310,14 @@ def _is_torch(x: Any) -> bool:
 
 
 def element_dtype(x: Any) -> np.dtype:
+    """The NumPy dtype of `x`'s elements; bfloat16 reports `core.BF16_TAG` (kind "V")."""
     if isinstance(x, Tensor):
-        return x.dtype.to_numpy()
-    if _is_torch(x):
+        dt = x.dtype
+    elif _is_torch(x):
         dt = core.dtype_from_torch(x.dtype)
-        return dt.to_numpy()
-    return np.asarray(x).dtype
+    else:
+        return np.asarray(x).dtype
+    return core.BF16_TAG if dt is core.bfloat16 else dt.to_numpy()
 
 
 def elem_dtype(x: Any) -> core.dtype:
@@ -343,9 +345,7 @@ def new_empty(x: Any, shape=None, dtype=None):
         return torch.empty(shape, dtype=tdt, device=x.device)
     if isinstance(x, Tensor):
         return empty(shape, x.dtype if dtype is None else _as_dtype(dtype))
-    npdt = np.asarray(x).dtype if dtype is None else np.dtype(dtype) if not isinstance(
-        dtype, core.dtype) else dtype.to_numpy()
-    return np.empty(shape, npdt)
+    return np.empty(shape, _numpy_storage(np.asarray(x).dtype if dtype is None else dtype))
 
 
 def new_zeros(x: Any, shape=None, dtype=None):
@@ -356,13 +356,21 @@ def new_zeros(x: Any, shape=None, dtype=None):
         return torch.zeros(shape, dtype=tdt, device=x.device)
     if isinstance(x, Tensor):
         return zeros(shape, x.dtype if dtype is None else _as_dtype(dtype))
-    npdt = np.asarray(x).dtype if dtype is None else np.dtype(dtype) if not isinstance(
-        dtype, core.dtype) else dtype.to_numpy()
-    return np.zeros(shape, npdt)
+    return np.zeros(shape, _numpy_storage(np.asarray(x).dtype if dtype is None else dtype))
+
+
+def _numpy_storage(dt) -> np.dtype:
+    """The NumPy storage dtype of element type `dt` (uint16 bit patterns for bfloat16)."""
+    if isinstance(dt, core.dtype):
+        return dt.to_numpy()
+    d = np.dtype(dt)
+    return core.bfloat16.to_numpy() if d.kind == "V" else d
 
 
 def _torch_dtype(dt):
     import torch
+    if not isinstance(dt, core.dtype) and not isinstance(dt, str):
+        dt = core.dtype_from_numpy(dt)
     if isinstance(dt, core.dtype):
         name = dt.long_name
     else:

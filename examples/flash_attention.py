@@ -4,6 +4,7 @@ import math
 
 import enceladus
 import enceladus.language as tl
+from enceladus_amd.configs import attention_configs
 
 
 @enceladus.jit
@@ -48,8 +49,16 @@ def attention_kernel(q_ptr, k_ptr, v_ptr, o_ptr, sm_scale, N_CTX, stride_h, stri
     o_desc.store([start_m * BLOCK_M, 0], acc.to(o_desc.dtype))
 
 
+def _check(q, k, v):
+    if not (tuple(q.shape) == tuple(k.shape) == tuple(v.shape)) or len(q.shape) != 4:
+        raise ValueError("q, k, and v must all have shape (batch, heads, seq_len, head_dim)")
+    if q.shape[-1] not in (16, 32, 64, 128):
+        raise ValueError(f"head_dim must be 16, 32, 64, or 128, not {q.shape[-1]}")
+
+
 def attention(q, k, v, causal: bool = False, sm_scale=None, o=None, block_m: int = 128,
               block_n: int = 64, num_warps: int = 4):
+    _check(q, k, v)
     z, h, n, d = q.shape
     o = enceladus.new_empty(q) if o is None else o
     scale = 1.0 / math.sqrt(d) if sm_scale is None else sm_scale
@@ -57,4 +66,28 @@ def attention(q, k, v, causal: bool = False, sm_scale=None, o=None, block_m: int
     attention_kernel[grid](q, k, v, o, scale, n, n * d, d, HEAD_DIM=d, BLOCK_M=block_m,
                            BLOCK_N=block_n, CAUSAL=causal, num_warps=num_warps,
                            dot_warps=(num_warps, 1))
+    return o
+
+
+def _prune(configs, named):
+    """The candidates `attention_configs` lists for this launch's dtype and head dimension."""
+    allowed = attention_configs(named["q_ptr"].dtype, named["HEAD_DIM"])
+    return [c for c in configs if c in allowed]
+
+
+attention_tuned_kernel = enceladus.autotune(
+    configs=attention_configs("float16", 128) + attention_configs("float32", 128),
+    key=["N_CTX", "HEAD_DIM", "CAUSAL"],
+    prune_configs_by={"early_config_prune": _prune},
+)(attention_kernel)
+
+
+def attention_tuned(q, k, v, causal: bool = False, sm_scale=None, o=None):
+    """`attention` with the tile the autotuner measures fastest for this shape."""
+    _check(q, k, v)
+    z, h, n, d = q.shape
+    o = enceladus.new_empty(q) if o is None else o
+    scale = 1.0 / math.sqrt(d) if sm_scale is None else sm_scale
+    grid = lambda meta: (enceladus.cdiv(n, meta["BLOCK_M"]), z * h)  # noqa: E731
+    attention_tuned_kernel[grid](q, k, v, o, scale, n, n * d, d, HEAD_DIM=d, CAUSAL=causal)
     return o

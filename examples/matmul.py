@@ -64,8 +64,11 @@ def _configs_for_dtype(configs, named):
     return [c for c in configs if c in allowed]
 
 
+# The candidate list is the union of the 16-bit and fp32 lists; pruning by the dtype of `a`
+# keeps each dtype's own tiles (the key includes the argument dtypes, so each dtype is tuned
+# separately).
 matmul_desc_tuned = enceladus.autotune(
-    configs=matmul_configs("float16"),
+    configs=matmul_configs("float16") + matmul_configs("float32"),
     key=["M", "N", "K"],
     prune_configs_by={"early_config_prune": _configs_for_dtype},
 )(matmul_desc_kernel)

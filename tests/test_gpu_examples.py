@@ -113,6 +113,10 @@ def test_histogram(n, bins, flush, monkeypatch):
     got = histogram(x, bins, 0.0, float(bins))
     assert np.array_equal(got, R.histogram(x, bins, 0.0, float(bins)))
     assert int(got.sum()) == n
+    # the launch ran the flush this case names: one level of global atomics, or two
+    from examples.histogram import histogram_kernel
+    ck = histogram_kernel.warmup(x, got, n, 0.0, 1.0, NUM_BINS=bins, BLOCK=1024)
+    assert (ck.gen.flush is None) == (flush == "atomic")
 
 
 @enceladus.jit
