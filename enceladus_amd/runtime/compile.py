@@ -191,6 +191,35 @@ class CompiledKernel:
                         fbuf, len(fk)))
         return out
 
+    def launch_noalloc(self, grid, kernarg: bytes, stream: int = 0):
+        """One logical launch of a kernel with a two-level flush through
+        `ek_launch_flush_noalloc`: the partial rows live in the library's static scratch
+        array, so nothing is allocated (for callers that cannot allocate). Raises HipError
+        when the launch needs more scratch than the array holds."""
+        import struct
+        fl = self.gen.flush
+        if not fl:
+            raise ValueError(f"{self.name} has no scratch buffer; launch it normally")
+        gx, gy, gz = (tuple(grid) + (1, 1, 1))[:3]
+        if gx == 0 or gy == 0 or gz == 0:
+            return
+        (gx, gy, gz), extra = self.launch_grid(grid)
+        if extra:
+            kernarg = kernarg[:self.packed_size] + extra
+            kernarg += b"\0" * ((-len(kernarg)) % 8)
+        offs = codegen_hip.arg_offsets(self.args)
+        bases = [struct.unpack_from("<Q", kernarg, offs[i])[0] for i in fl["bases"]]
+        fargs = [codegen_hip.KernelArg("p", "ptr", None, "int32_t*"),
+                 codegen_hip.KernelArg("n", "scalar", None, "int32_t")] + \
+            [codegen_hip.KernelArg("h", "ptr", None, "int32_t*") for _ in bases]
+        fk = codegen_hip.pack_args(fargs, [0, gx, *bases])
+        kb = ctypes.create_string_buffer(kernarg, len(kernarg))
+        fb = ctypes.create_string_buffer(fk, len(fk))
+        hip.call("ek_launch_flush_noalloc", ctypes.c_void_p(stream or None), self.function(),
+                 gx, gy, gz, self.gen.block, kb, len(kernarg), offs[-1],
+                 self._flush_function(), fl["chunks"], (gx + fl["rb"] - 1) // fl["rb"], 256,
+                 fb, len(fk), 0, gx * fl["total"] * 4)
+
     def launch_grid(self, grid):
         """(launch grid, extra kernarg bytes) for a logical program grid."""
         gx, gy, gz = (tuple(grid) + (1, 1, 1))[:3]

@@ -87,7 +87,15 @@ _SIGS = {
     "ek_timed_launch": [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_uint32] * 7 +
                        [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
                         ctypes.POINTER(ctypes.c_float)],
+    "ek_launch_flush_noalloc": [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_uint32] * 4 +
+                               [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_size_t,
+                                ctypes.c_void_p] + [ctypes.c_uint32] * 3 +
+                               [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_size_t,
+                                ctypes.c_size_t],
 }
+
+# The size of the no-allocation launch's static scratch array (EK_SCRATCH_BYTES).
+SCRATCH_BYTES = 16 << 20
 
 EXPORTED = sorted([*_SIGS, "ek_compile", "ek_buffer_free", "ek_version", "ek_runtime_version"])
 

@@ -101,6 +101,28 @@ int ek_timed_launch(void* stream, void* function, uint32_t gx, uint32_t gy, uint
                     size_t kernarg_size, int reps, float* ms_per_launch, char* err,
                     size_t errlen);
 
+/* No counterpart in the reference. For callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): launches a
+ * kernel that keeps per-workgroup partial results in a scratch buffer (a privatised-bin
+ * kernel), then its second flush level, exactly as the allocating path does with two
+ * ek_launch calls and a library-allocated partial buffer, but with the scratch in this
+ * library's static device array of EK_SCRATCH_BYTES per GPU (held until the process ends).
+ * `kernarg` / `flush_kernarg` are packed as for ek_launch; the scratch address is written
+ * at byte offset `scratch_offset` / `flush_scratch_offset` (8-byte aligned) of copies of
+ * them. Block sizes are 1-D. Fails, launching nothing, when `scratch_bytes` exceeds
+ * EK_SCRATCH_BYTES. Calls no allocating routine. Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (other streams, other threads) race; calls in one
+ * stream's order do not. The kernels write every partial word they read, so nothing needs
+ * clearing between calls. */
+#define EK_SCRATCH_BYTES (16u << 20)
+int ek_launch_flush_noalloc(void* stream, void* function, uint32_t gx, uint32_t gy,
+                            uint32_t gz, uint32_t block, const void* kernarg,
+                            size_t kernarg_size, size_t scratch_offset, void* flush_function,
+                            uint32_t fgx, uint32_t fgy, uint32_t fblock,
+                            const void* flush_kernarg, size_t flush_kernarg_size,
+                            size_t flush_scratch_offset, size_t scratch_bytes, char* err,
+                            size_t errlen);
+
 /* Version string of the shim and of the HIP runtime it runs on. */
 const char* ek_version(void);
 int ek_runtime_version(int* version);
