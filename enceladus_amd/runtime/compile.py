@@ -25,7 +25,7 @@ import sys
 import threading
 from pathlib import Path
 
-from enceladus_amd.compiler import codegen_hip, frontend, ir, rewrite, widen
+from enceladus_amd.compiler import codegen_hip, frontend, ir, rewrite, simplify, verify, widen
 from enceladus_amd.runtime import hip
 
 log = logging.getLogger("enceladus")
@@ -278,10 +278,19 @@ def compile_ir(fn: ir.Func, options: dict | None = None) -> CompiledKernel:
 
 
 def build_module(jfn, arg_types, arg_facts, constexprs, num_warps, options) -> ir.Func:
+    """Frontend, then the IR passes in order (reference: compiler/pipeline.py:14-38); with
+    ENCELADUS_VERIFY=1 the IR is verified after each stage."""
     fn = frontend.build_ir(jfn.fn, arg_types, arg_facts, constexprs, num_warps, options)
+    verify.maybe_verify(fn, "the frontend")
+    if not (options or {}).get("no_simplify"):
+        simplify.simplify(fn)
+        verify.maybe_verify(fn, "the simplifier")
     if widen.needs_idx64(fn):
         widen.widen_index_math(fn)
+        verify.maybe_verify(fn, "64-bit index widening")
     if not (options or {}).get("no_scale_fold"):
         rewrite.fold_softmax_scale(fn)
+        verify.maybe_verify(fn, "the attention scale rewrite")
     ir.dce(fn)
+    verify.maybe_verify(fn, "dead-code elimination")
     return fn

@@ -14,6 +14,8 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 os.environ.setdefault("ENCELADUS_CACHE_DIR", os.path.join(ROOT, ".ek_cache"))
+# every kernel the tests compile has its IR verified after each compiler stage
+os.environ.setdefault("ENCELADUS_VERIFY", "1")
 
 TOL = {"float32": (1e-5, 1e-5), "float16": (1e-3, 2e-3), "bfloat16": (1e-2, 1.6e-2)}
 
