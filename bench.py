@@ -23,7 +23,8 @@ core) on a random sample of each grid's programs, and NumPy's closed form (the e
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME[,NAME]]
                        [--no-cpu-baseline]
-NAME is a workload of examples/workloads.py, or copy_calib (the counter calibration copy).
+NAME is a workload of examples/workloads.py, copy_calib (the counter calibration copy) or
+launch_overhead (host cost of warm launches; part of the default run).
 """
 
 from __future__ import annotations
@@ -182,6 +183,52 @@ def copy_calibration(torch, timer, steps):
     return {"name": "copy_calib", "config": "torch copy 256 MiB -> 256 MiB", "ms": ms,
             "bytes": 8 * n, "gbps": 8 * n / ms / 1e6, "bound": "hbm", "dtype": "fp32",
             "kernel": "copy", "roofline_frac": 8 * n / ms / 1e6 * 1e9 / HBM_PEAK}
+
+
+def launch_overhead(torch, reps=5, n_launch=10_000):
+    """Host cost of a warm launch (reference: benchmarks/bench_dispatch.py): µs per launch
+    for back-to-back `@jit` launches of a 1024-element vector add through the Python front
+    door (`kernel[grid](...)`, torch-ROCm tensors), the same kernel through a pre-packed
+    `ek_launch` (the native floor), `torch.add(out=)`, and a launch + synchronize round
+    trip. Medians over `reps` runs."""
+    import statistics
+
+    from examples.vector_add import add_kernel
+    n = 1024
+    x, y, o = (torch.randn(n, device="cuda") for _ in range(3))
+
+    def jit_launch():
+        add_kernel[(1,)](x, y, o, n, BLOCK=1024)
+
+    native = make_launch(add_kernel, (1,), (x, y, o, n), {"BLOCK": 1024})
+
+    def sustained(fn, count=n_launch):
+        out = []
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(count):
+                fn()
+            torch.cuda.synchronize()
+            out.append((time.perf_counter() - t0) / count * 1e6)
+        return statistics.median(out)
+
+    def round_trip(fn, count=300):
+        out = []
+        for _ in range(count):
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            out.append((time.perf_counter() - t0) * 1e6)
+        return statistics.median(out)
+
+    jit_launch()
+    sustained(jit_launch, 2000)                  # warm the clocks and caches
+    return {"jit_sustained_us": round(sustained(jit_launch), 2),
+            "native_ek_launch_sustained_us": round(sustained(native), 2),
+            "torch_add_sustained_us": round(sustained(lambda: torch.add(x, y, out=o)), 2),
+            "jit_round_trip_us": round(round_trip(jit_launch), 2),
+            "workload": "vector add n=1024, grid (1,), BLOCK 1024, torch-ROCm tensors"}
 
 
 def tuned_named(tuned, args, fixed):
@@ -389,6 +436,8 @@ def main():
     cpu = {}
     for n in names:
         log(f"[bench] {n} ...")
+        if n == "launch_overhead":
+            continue
         if n == "copy_calib":
             results[n] = copy_calibration(torch, timer, args.steps)
             log(f"[bench] copy_calib: {results[n]['gbps']:.0f} GB/s")
@@ -407,6 +456,10 @@ def main():
                 f"numpy {cpu[n]['numpy']['value']:.4g}")
         del host
         torch.cuda.empty_cache()
+    if not results:         # only the launch-overhead rows were asked for
+        print(json.dumps({"metric": "warm launch overhead (us per launch)",
+                          "launch_overhead": launch_overhead(torch)}), flush=True)
+        return
     real = {k: r for k, r in results.items() if k != "copy_calib"} or results
     head = real.get("softmax") or next(iter(real.values()))
     line = {
@@ -428,6 +481,10 @@ def main():
         "workloads": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
                           for kk, vv in v.items()} for k, v in results.items()},
     }
+    if not args.only or "launch_overhead" in names:
+        log("[bench] launch overhead ...")
+        line["launch_overhead"] = launch_overhead(torch)
+        log(f"    {line['launch_overhead']}")
     if cpu:
         hc = cpu.get(head["name"]) or next(iter(cpu.values()))
         ib = hc["interpreter"]

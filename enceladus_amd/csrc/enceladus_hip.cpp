@@ -11,6 +11,16 @@
 #include <string>
 #include <vector>
 
+// The HIP runtime's launch with dispatch-boundary events (declared in hip/hip_ext.h, whose
+// kernel-launch templates need the HIP compiler; this file is host code built by g++).
+extern "C" hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t globalWorkSizeX,
+                                               uint32_t globalWorkSizeY, uint32_t globalWorkSizeZ,
+                                               uint32_t localWorkSizeX, uint32_t localWorkSizeY,
+                                               uint32_t localWorkSizeZ, size_t sharedMemBytes,
+                                               hipStream_t hStream, void** kernelParams,
+                                               void** extra, hipEvent_t startEvent,
+                                               hipEvent_t stopEvent, uint32_t flags);
+
 namespace {
 
 int fail(char* err, size_t errlen, const std::string& msg) {
@@ -160,6 +170,26 @@ int ek_launch(void* stream, void* function, uint32_t gx, uint32_t gy, uint32_t g
   EK_CHECK(hipModuleLaunchKernel(static_cast<hipFunction_t>(function), gx, gy, gz, bx, by,
                                  bz, dyn_lds, static_cast<hipStream_t>(stream), nullptr,
                                  config));
+  return 0;
+}
+
+int ek_launch_timed_events(void* stream, void* function, uint32_t gx, uint32_t gy,
+                           uint32_t gz, uint32_t bx, uint32_t by, uint32_t bz,
+                           uint32_t dyn_lds, void* kernarg, size_t kernarg_size,
+                           void* start_event, void* stop_event, char* err, size_t errlen) {
+  const uint64_t tx = (uint64_t)gx * bx, ty = (uint64_t)gy * by, tz = (uint64_t)gz * bz;
+  if (tx > 0xFFFFFFFFull || ty > 0xFFFFFFFFull || tz > 0xFFFFFFFFull) {
+    return fail(err, errlen, "ek_launch_timed_events: more than 2^32 threads along one "
+                             "dimension; time this launch with ek_event_record instead");
+  }
+  size_t size = kernarg_size;
+  void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, kernarg, HIP_LAUNCH_PARAM_BUFFER_SIZE,
+                    &size, HIP_LAUNCH_PARAM_END};
+  EK_CHECK(hipExtModuleLaunchKernel(static_cast<hipFunction_t>(function), (uint32_t)tx,
+                                    (uint32_t)ty, (uint32_t)tz, bx, by, bz, dyn_lds,
+                                    static_cast<hipStream_t>(stream), nullptr, config,
+                                    static_cast<hipEvent_t>(start_event),
+                                    static_cast<hipEvent_t>(stop_event), 0));
   return 0;
 }
 

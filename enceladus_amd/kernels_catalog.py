@@ -89,7 +89,6 @@ def compile_all(verbose: bool = False) -> int:
     pool: each program is its own hiprtc object, and ctypes releases the GIL)."""
     from concurrent.futures import ThreadPoolExecutor
 
-    from enceladus_amd.runtime import compile as C
     jobs = []
     seen = set()
     for kern, args, kw in specs() + table_specs():
@@ -105,11 +104,9 @@ def compile_all(verbose: bool = False) -> int:
         jobs.append((kern, types, facts, consts, nw, dw))
 
     def one(job):
+        # the launch path's own compile: also records the specialization-cache entry
         kern, types, facts, consts, nw, dw = job
-        options = {"dot_warps": tuple(dw) if dw else None, "debug": False}
-        fn = C.build_module(kern, types, facts, consts, nw, options)
-        ck = C.compile_ir(fn, options)
-        return ck
+        return kern._compile_for(types, facts, consts, nw, dw).ck
 
     with ThreadPoolExecutor(max_workers=8) as ex:
         for ck in ex.map(one, jobs):

@@ -3,10 +3,13 @@
 On the first launch for a key, every candidate config is compiled (in a thread pool:
 hiprtc programs are per-call objects) and timed with HIP events on the launch stream:
 phase 1 times each config, phase 2 times the few fastest again in interleaved rounds, and
-the earliest finalist within `tolerance` of the fastest wins (the reference's rule). The
-winner is kept in memory and merged, under a file lock, into
-`$ENCELADUS_CACHE_DIR/autotune/<kernel and compiler hash>/<arch>.json`; a saved winner that
-is no longer a candidate is re-tuned, and a compiler change starts a new file. Arguments in
+the earliest finalist within `tolerance` of the fastest wins (the reference's rule). Each
+sample is the GPU time of the launch's dispatches alone (`testing.do_bench`). The winner is
+kept in memory and appended to the kernel's tuning log (`TuneLog`,
+`$ENCELADUS_CACHE_DIR/autotune/<kernel>-<source and compiler hash>/<arch>.jsonl`); a logged
+winner that is no longer a candidate is re-tuned, and a compiler change starts a new log.
+One method, `_resolve`, decides every launch's config (memory, then the log, then tuning or,
+for `warmup`/`explain`, the first candidate). Arguments in
 `restore_value` are restored and those in `reset_to_zero` zeroed before every timed run
 and after tuning, so in-place kernels don't accumulate. Configs that fail to compile or
 run are skipped with a warning.
@@ -111,16 +114,9 @@ _DTYPE_NAMES = {"float16", "float32", "bfloat16", "int8", "int16", "int32", "int
 
 
 def _compiler_hash() -> str:
-    """Changes whenever the code generator or the device templates change."""
-    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-    h = hashlib.sha256()
-    for sub in ("compiler", os.path.join("csrc", "include")):
-        d = os.path.join(root, sub)
-        for name in sorted(os.listdir(d)):
-            if name.endswith((".py", ".h")):
-                with open(os.path.join(d, name), "rb") as f:
-                    h.update(f.read())
-    return h.hexdigest()[:16]
+    """Changes whenever the code generator, the device templates or the runtime change."""
+    from enceladus_amd.runtime.speccache import compiler_hash
+    return compiler_hash()
 
 
 # -- argument state around timed runs ----------------------------------------------
@@ -158,6 +154,57 @@ def _zero(v) -> None:
             hip.call("ek_memset", ctypes.c_void_p(v.ptr), 0, v.nbytes, None)
 
 
+class TuneLog:
+    """The tuning results of one kernel source under one compiler, on disk.
+
+    One JSON object per line, appended as results are found: `{"key", "config",
+    "timings_ms"}`; a later line for a key supersedes an earlier one. Lines go out with one
+    `write` on a descriptor opened for appending, under an exclusive `flock`, so processes
+    tuning the same kernel at once interleave whole lines. A compiler change writes a new
+    file (the compiler hash is in the path); a line that does not parse is skipped.
+    """
+
+    def __init__(self, path):
+        self.path = path
+        self._records: dict | None = None
+
+    def _read(self) -> dict:
+        if self._records is None:
+            self._records = {}
+            if os.environ.get("ENCELADUS_ALWAYS_COMPILE") != "1":
+                try:
+                    text = self.path.read_text()
+                except OSError:
+                    text = ""
+                for line in text.splitlines():
+                    with contextlib.suppress(ValueError, KeyError, TypeError):
+                        rec = json.loads(line)
+                        self._records[rec["key"]] = Config.from_json(rec["config"])
+        return self._records
+
+    def get(self, key: str):
+        return self._read().get(key)
+
+    def put(self, key: str, cfg: "Config", timings: dict) -> None:
+        self._read()[key] = cfg
+        line = json.dumps({"key": key, "config": cfg.to_json(),
+                           "timings_ms": timings}, sort_keys=True) + "\n"
+        try:
+            import fcntl
+            self.path.parent.mkdir(parents=True, exist_ok=True)
+            fd = os.open(self.path, os.O_WRONLY | os.O_APPEND | os.O_CREAT, 0o644)
+            try:
+                fcntl.flock(fd, fcntl.LOCK_EX)
+                os.write(fd, line.encode())
+            finally:
+                os.close(fd)
+        except OSError as e:
+            log.debug("couldn't record the tuning result: %s", e)
+
+    def entries(self) -> dict:
+        return dict(self._read())
+
+
 class Autotuner:
     def __init__(self, fn, configs, key, prune_configs_by=None, reset_to_zero=None,
                  restore_value=None, warmup_ms=50, rep=20, tolerance=0.01):
@@ -172,8 +219,7 @@ class Autotuner:
         self.tolerance = tolerance
         self.best: dict[str, Config] = {}
         self.timings: dict[str, dict] = {}
-        self._saved: dict[str, Config] = {}
-        self._loaded = False
+        self._log: TuneLog | None = None
         self._lock = threading.Lock()
         self.__name__ = getattr(fn, "__name__", "kernel")
         self._ek_jit = False
@@ -189,7 +235,7 @@ class Autotuner:
     def __getitem__(self, grid):
         return lambda *args, **kwargs: self.run(*args, grid=grid, **kwargs)
 
-    # -- keys and persistence ------------------------------------------------------
+    # -- keys and the tuning log ---------------------------------------------------
     def _key(self, named: dict) -> str:
         from enceladus_amd.runtime import tensor as T
         parts = [_key_value(named.get(k)) for k in self.key]
@@ -197,50 +243,40 @@ class Autotuner:
                if n in named and T.is_array_like(named[n])]
         return "|".join(parts) + "|" + ",".join(dts)
 
-    def _path(self):
+    def log_path(self):
+        """`$ENCELADUS_CACHE_DIR/autotune/<kernel>-<hash of its source and the compiler>/
+        <arch>.jsonl`."""
         from enceladus_amd.runtime.compile import ARCH, cache_dir
         src = inspect.getsource(_jit_of(self.fn).fn)
         h = hashlib.sha256((src + _compiler_hash()).encode()).hexdigest()[:24]
-        return cache_dir() / "autotune" / f"{self.__name__}-{h}" / f"{ARCH}.json"
+        return cache_dir() / "autotune" / f"{self.__name__}-{h}" / f"{ARCH}.jsonl"
 
-    def _load(self):
-        self._loaded = True
-        if os.environ.get("ENCELADUS_ALWAYS_COMPILE") == "1":
-            return
-        try:
-            data = json.loads(self._path().read_text())
-        except (OSError, ValueError):
-            return
-        for k, v in data.items():
-            with contextlib.suppress(KeyError, TypeError, ValueError):
-                self._saved.setdefault(k, Config.from_json(v))
+    @property
+    def tune_log(self) -> TuneLog:
+        path = self.log_path()
+        if self._log is None or self._log.path != path:
+            self._log = TuneLog(path)
+        return self._log
 
-    def _from_saved(self, key: str, named: dict):
-        """The candidate matching the saved winner for `key` (keeping its pre_hook); a
-        saved winner that is no longer a candidate is re-tuned."""
-        saved = self._saved.pop(key, None)
-        if saved is None:
-            return None
-        return next((c for c in self._candidates(named) if c == saved), None)
-
-    def _save(self):
-        import fcntl
-        p = self._path()
-        try:
-            p.parent.mkdir(parents=True, exist_ok=True)
-            with open(p.with_suffix(".lock"), "a") as lock:
-                fcntl.flock(lock, fcntl.LOCK_EX)
-                data: dict = {}
-                with contextlib.suppress(OSError, ValueError):
-                    loaded = json.loads(p.read_text())
-                    if isinstance(loaded, dict):
-                        data = loaded
-                data.update({k: c.to_json() for k, c in self.best.items()})
-                tmp = p.with_suffix(f".tmp{os.getpid()}.{threading.get_ident()}")
-                tmp.write_text(json.dumps(data, indent=1, sort_keys=True))
-                os.replace(tmp, p)
-        except OSError as e:
-            log.debug("couldn't save autotuning results: %s", e)
+    def _resolve(self, named: dict, tune):
+        """The config for this launch: tuned in this process, recorded in the tuning log
+        (when it is still a candidate), tuned now when `tune` is a callable that tunes,
+        or else the first candidate."""
+        key = self._key(named)
+        cfg = self.best.get(key)
+        if cfg is not None:
+            return cfg
+        with self._lock:
+            cfg = self.best.get(key)
+            if cfg is None:
+                logged = self.tune_log.get(key)
+                if logged is not None:
+                    cfg = next((c for c in self._candidates(named) if c == logged), None)
+            if cfg is None and tune is not None:
+                cfg = tune(key)
+            if cfg is not None:
+                self.best[key] = cfg
+        return cfg if cfg is not None else self._candidates(named)[0]
 
     # -- candidates ----------------------------------------------------------------
     def _candidates(self, named: dict) -> list:
@@ -263,43 +299,22 @@ class Autotuner:
         """The tuned config for these launch arguments, or None if not tuned yet."""
         return self.best.get(self._key(_named(self.fn, args, kwargs)))
 
-    def _config_without_tuning(self, args, kwargs) -> Config:
-        if not self._loaded:
-            self._load()
-        named = _named(self.fn, args, kwargs)
-        key = self._key(named)
-        with self._lock:
-            cfg = self.best.get(key)
-            if cfg is None:
-                cfg = self._from_saved(key, named)
-                if cfg is not None:
-                    self.best[key] = cfg
-        return cfg if cfg is not None else self._candidates(named)[0]
-
     def warmup(self, *args, **kwargs):
-        """Compiles (never benchmarks) with the tuned config, or the first candidate."""
-        cfg = self._config_without_tuning(args, kwargs)
+        """Compiles (never benchmarks) with the tuned or logged config, or the first
+        candidate."""
+        cfg = self._resolve(_named(self.fn, args, kwargs), None)
         return self.fn.warmup(*args, **kwargs, **cfg.kwargs, **cfg.launch_options())
 
     def explain(self, *args, **kwargs) -> str:
-        cfg = self._config_without_tuning(args, kwargs)
+        cfg = self._resolve(_named(self.fn, args, kwargs), None)
         return self.fn.explain(*args, **kwargs, **cfg.kwargs, **cfg.launch_options())
 
     # -- launching and tuning ------------------------------------------------------
     def run(self, *args, grid, **kwargs):
-        if not self._loaded:
-            self._load()
         named = _named(self.fn, args, kwargs)
-        key = self._key(named)
-        cfg = self.best.get(key)
-        if cfg is None:
-            with self._lock:
-                cfg = self.best.get(key) or self._from_saved(key, named)
-                if cfg is None:
-                    cfg = self._tune(key, args, kwargs, grid, named)
-                self.best[key] = cfg
+        cfg = self._resolve(named, lambda key: self._tune(key, args, kwargs, grid, named))
         if os.environ.get("ENCELADUS_PRINT_AUTOTUNING", "0") not in ("", "0"):
-            print(f"autotune {self.__name__} [{key}]: {cfg}")
+            print(f"autotune {self.__name__} [{self._key(named)}]: {cfg}")
         if cfg.pre_hook:
             cfg.pre_hook(named)
         return self.fn.run(*args, grid=grid, **cfg.kwargs, **cfg.launch_options(), **kwargs)
@@ -381,9 +396,8 @@ class Autotuner:
         fastest = min(timings[i] for i in pool)
         best_i = min(i for i in pool if timings[i] <= fastest * (1 + self.tolerance))
         best = cfgs[best_i]
-        self.best[key] = best
         self.timings[key] = {repr(cfgs[i]): t for i, t in timings.items()}
-        self._save()
+        self.tune_log.put(key, best, self.timings[key])
         return best
 
 

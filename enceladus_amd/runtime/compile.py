@@ -2,8 +2,8 @@
 
 `compile_specialization` builds IR, runs the HIP emitter, compiles with hiprtc for gfx950
 and caches the code object under `$ENCELADUS_CACHE_DIR` (default
-`~/.cache/enceladus_amd`), keyed by the generated source, the compile options and the
-shim/header versions. Reference: src/enceladus/runtime/compile.py:38-164 and cache.py:26-144
+`~/.cache/enceladus_amd`), keyed by the generated source, the compile options, the device
+header and the shim and HIP runtime versions. Reference: src/enceladus/runtime/compile.py:38-164 and cache.py:26-144
 (disk cache of compiled kernels, corrupt entries recompiled).
 
 Environment variables (reference: src/enceladus/runtime/compile.py:6-10):
@@ -44,8 +44,17 @@ def cache_dir() -> Path:
 
 
 def _header_hash() -> str:
+    """The device header, the shim's version and the HIP runtime's (hiprtc ships with it):
+    a code object compiled under another of them is not reused."""
     h = hashlib.sha256()
     h.update((hip.INCLUDE_DIR / "enceladus_cdna4.h").read_bytes())
+    try:
+        lib = hip.load_library()
+        v = ctypes.c_int(0)
+        lib.ek_runtime_version(ctypes.byref(v))
+        h.update(f"{lib.ek_version().decode()}|{v.value}".encode())
+    except Exception:  # noqa: BLE001 - the shim is missing: compiling fails loudly later
+        pass
     return h.hexdigest()[:16]
 
 
@@ -231,11 +240,15 @@ class CompiledKernel:
         return (min(total, cap), 1, 1), struct.pack("<iii", gx, gy, gz)
 
     def launch_raw(self, grid, kernarg: bytes, stream: int = 0):
-        from enceladus_amd.runtime import debug
+        from enceladus_amd.runtime import debug, timing
+        timer = timing.current()
         for fn_, g_, blk, buf, n in self.prepare(grid, kernarg, stream):
             t0 = debug.before_launch(stream) if debug._active is not None else None
-            hip.call("ek_launch", ctypes.c_void_p(stream or None), fn_, g_[0], g_[1], g_[2],
-                     blk, 1, 1, 0, buf, n)
+            if timer is not None:
+                timer.launch(stream, fn_, g_, blk, buf, n)
+            else:
+                hip.call("ek_launch", ctypes.c_void_p(stream or None), fn_, g_[0], g_[1],
+                         g_[2], blk, 1, 1, 0, buf, n)
             if t0 is not None:
                 nm = self.name if fn_ is self._function else self.gen.flush["name"]
                 debug.after_launch(t0, stream, nm, g_, blk,

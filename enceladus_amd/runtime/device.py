@@ -58,13 +58,22 @@ def synchronize() -> None:
     tensor.flush_pending()
 
 
+_raw_stream = None
+
+
 def current_stream() -> int:
     """The HIP stream launches go to: torch's current stream when torch is in use."""
+    global _raw_stream
     import sys
     torch = sys.modules.get("torch")
     if torch is not None:
         try:
             if torch.cuda.is_initialized():
+                if _raw_stream is None:
+                    # torch's raw-handle accessor skips building a Stream object
+                    _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", False)
+                if _raw_stream:
+                    return int(_raw_stream(torch.cuda.current_device()))
                 return int(torch.cuda.current_stream().cuda_stream)
         except Exception:  # noqa: BLE001
             pass

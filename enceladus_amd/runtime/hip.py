@@ -87,6 +87,9 @@ _SIGS = {
     "ek_timed_launch": [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_uint32] * 7 +
                        [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
                         ctypes.POINTER(ctypes.c_float)],
+    "ek_launch_timed_events": [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_uint32] * 7 +
+                              [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                               ctypes.c_void_p],
     "ek_launch_flush_noalloc": [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_uint32] * 4 +
                                [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_size_t,
                                 ctypes.c_void_p] + [ctypes.c_uint32] * 3 +

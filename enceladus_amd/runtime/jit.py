@@ -16,6 +16,7 @@ import ctypes
 import inspect
 import os
 import struct
+import threading
 from dataclasses import dataclass
 from typing import Any, Callable
 
@@ -26,6 +27,10 @@ from enceladus_amd.compiler.errors import CompilationError, DeviceAssertionError
 from enceladus_amd.language import core
 from enceladus_amd.runtime import compile as C
 from enceladus_amd.runtime import device as D
+from enceladus_amd.runtime import hip as _hip
+from enceladus_amd.runtime import speccache
+from enceladus_amd.runtime import debug as _trace
+from enceladus_amd.runtime import timing as _timing
 from enceladus_amd.runtime import tensor as T
 
 
@@ -110,6 +115,91 @@ def arg_facts(value: Any) -> dict:
 MAX_ELEMENT_INDEX = (1 << 31) - 1
 # facts that stay in the specialization even for do_not_specialize parameters
 REQUIRED_FACTS = ("idx64", "span2g")
+
+# -- the warm launch path ------------------------------------------------------------
+# A warm launch of a specialization whose arguments are all device arrays and scalars is
+# keyed by a tuple computed in one pass over the arguments (dtypes, 16-byte alignment, a
+# span class, integer width classes, float signs, constexpr values, launch options and
+# the environment switches that change code generation), and packs its kernarg with a
+# precomputed `struct.Struct`. Launches with NumPy arrays, assertion buffers, coarsened
+# program walks or a second flush kernel take the general path.
+
+_ENV = getattr(os.environ, "_data", None)      # POSIX: bytes keys, updated by os.environ
+_ENV_KEYS = (b"ENCELADUS_CODEGEN", b"ENCELADUS_OVERRIDE_DIR", b"ENCELADUS_DEBUG",
+             b"ENCELADUS_INTERPRET")
+
+
+def _env_token() -> tuple:
+    e = _ENV
+    if e is None:
+        return tuple(os.environ.get(k.decode()) for k in _ENV_KEYS)
+    return (e.get(b"ENCELADUS_CODEGEN"), e.get(b"ENCELADUS_OVERRIDE_DIR"),
+            e.get(b"ENCELADUS_DEBUG"), e.get(b"ENCELADUS_INTERPRET"))
+
+
+_torch_mod = None
+
+
+def _torch():
+    """torch, once something imported it (this module never imports it)."""
+    global _torch_mod
+    if _torch_mod is None:
+        import sys
+        _torch_mod = sys.modules.get("torch")
+    return _torch_mod
+
+
+def _span_class(nbytes_last: int, last: int) -> int:
+    """0: small; 1: >= 2 GiB of bytes (no buffer loads); 2: also > 2^31 - 1 elements."""
+    if last > MAX_ELEMENT_INDEX:
+        return 2
+    return 1 if nbytes_last >= (1 << 31) - 64 else 0
+
+
+def _int_class(v: int) -> int:
+    if -(1 << 31) <= v < (1 << 31):
+        return 0
+    if -(1 << 63) <= v < (1 << 63):
+        return 1
+    return 2
+
+
+_FMT = {"int32_t": ("i", 4), "int64_t": ("q", 8), "uint32_t": ("I", 4), "uint64_t": ("Q", 8),
+        "float": ("f", 4), "int16_t": ("h", 2), "uint16_t": ("H", 2), "int8_t": ("b", 1),
+        "uint8_t": ("B", 1)}
+
+
+class _FastEntry:
+    """A specialization's pre-packed launch: kernarg struct, function, block size."""
+
+    __slots__ = ("lc", "st", "fn", "block")
+
+    def __init__(self, lc, st, fn, block):
+        self.lc, self.st, self.fn, self.block = lc, st, fn, block
+
+
+def _fast_entry(lc) -> "_FastEntry | None":
+    g = lc.ck.gen
+    if g.flush or g.coarsen or g.asserts:
+        return None
+    fmt, off = "<", 0
+    for ka in lc.ck.args:
+        code, size = ("Q", 8) if ka.kind == "ptr" else _FMT[ka.cparam]
+        pad = (-off) % size
+        fmt += "x" * pad + code
+        off += pad + size
+    fmt += "x" * ((-off) % 8)
+    return _FastEntry(lc, struct.Struct(fmt), lc.ck.function(), g.block)
+
+
+_tls = threading.local()
+
+
+def _errbuf():
+    b = getattr(_tls, "err", None)
+    if b is None:
+        b = _tls.err = ctypes.create_string_buffer(1024)
+    return b
 
 
 def _last_index(value) -> int:
@@ -204,20 +294,18 @@ class Launcher:
         return True
 
     def __call__(self, grid, values: list, stream: int | None = None):
-        bindings = []
-        packed = []
-        for i, v in enumerate(values):
-            if T.is_array_like(v):
-                if i in self.writes and isinstance(v, np.ndarray) and not v.flags.writeable:
-                    raise ValueError(
-                        f"argument `{self.runtime_names[i]}` is a read-only NumPy array, and "
-                        "the kernel writes it; pass a writable array (for example a copy)")
-                b = T.bind_array(v)
-                b.writeback = i in self.writes
-                bindings.append(b)
-                packed.append(b.ptr)
-            else:
-                packed.append(v)
+        arrays = [i for i, v in enumerate(values) if T.is_array_like(v)]
+        for i in arrays:
+            v = values[i]
+            if i in self.writes and isinstance(v, np.ndarray) and not v.flags.writeable:
+                raise ValueError(
+                    f"argument `{self.runtime_names[i]}` is a read-only NumPy array, and "
+                    "the kernel writes it; pass a writable array (for example a copy)")
+        ptrs, bindings = T.bind_arrays([values[i] for i in arrays],
+                                       {k for k, i in enumerate(arrays) if i in self.writes})
+        packed = list(values)
+        for i, p in zip(arrays, ptrs):
+            packed[i] = p
         if stream is None:
             stream = D.current_stream()
         asserts = self.ck.gen.asserts
@@ -266,7 +354,9 @@ class JITFunction:
                 p.default if p.default is not inspect.Parameter.empty else inspect.Parameter.empty,
                 p.name in dns or i in dns))
         self.arg_names = [p.name for p in self.params]
+        self._name_set = frozenset(self.arg_names)
         self._cache: dict[Any, Launcher] = {}
+        self._fast: dict[Any, _FastEntry] = {}
 
     def __repr__(self):
         return f"JITFunction({self.fn.__module__}:{self.__name__})"
@@ -346,10 +436,24 @@ class JITFunction:
             options[k.strip()] = int(v) if v.isdigit() else (v if v else True)
         # ENCELADUS_DEBUG=1 keeps tl.device_assert checks (part of the key below)
         options["debug"] = _debug()
+        # a specialization an earlier process compiled skips the frontend and codegen
+        plain = not (os.environ.get("ENCELADUS_OVERRIDE_DIR") or
+                     os.environ.get("ENCELADUS_DUMP", "0") not in ("", "0"))
+        skey = speccache.spec_key(self, types, facts, consts, num_warps, options) \
+            if plain else None
+        if skey is not None:
+            hit = speccache.load(skey)
+            if hit is not None:
+                gen, ir_text, names, writes, deps = hit
+                ck = C.CompiledKernel(gen, ir_text, C.compile_code(gen.source, gen.name))
+                return Launcher(ck, names, writes, consts, deps)
         fn_ir = C.build_module(self, types, facts, consts, num_warps, options)
         ck = C.compile_ir(fn_ir, options)
         runtime_names = list(types.keys())
-        return Launcher(ck, runtime_names, _writes(fn_ir), consts, getattr(fn_ir, "deps", ()))
+        writes = _writes(fn_ir)
+        if skey is not None:
+            speccache.store(skey, fn_ir, ck.gen, runtime_names, writes)
+        return Launcher(ck, runtime_names, writes, consts, getattr(fn_ir, "deps", ()))
 
     def _lookup(self, vals, num_warps, dot_warps) -> Launcher:
         types, facts, consts = self.specialize(vals)
@@ -362,8 +466,110 @@ class JITFunction:
             self._cache[key] = lc
         return lc
 
+    def _fast_key(self, args, kwargs, num_warps, dot_warps):
+        """(key, runtime values) for the warm path, or None when an argument needs the
+        general path (NumPy arrays, unknown or missing arguments, unhashable constexprs)."""
+        for k in kwargs:
+            if k not in self._name_set:
+                return None
+        torch = _torch()
+        tt = torch.Tensor if torch else ()
+        n = len(args)
+        key = [num_warps, dot_warps, _env_token()]
+        rt = []
+        for p in self.params:
+            if p.index < n:
+                v = args[p.index]
+            elif p.name in kwargs:
+                v = kwargs[p.name]
+            elif p.default is not inspect.Parameter.empty:
+                v = p.default
+            else:
+                return None
+            t = type(v)
+            if p.is_constexpr:
+                c = core.unwrap(v)
+                tc = type(c)
+                if tc is float:
+                    key.append((tc, struct.pack("<d", c)))
+                elif tc in (int, bool, str) or isinstance(c, core.dtype):
+                    key.append((tc, c))
+                else:
+                    try:
+                        key.append((tc, hash(c), c))
+                    except TypeError:
+                        return None
+                continue
+            if t is int:
+                key.append((int, v & 15 == 0, v == 1, _int_class(v)))
+                rt.append(v)
+            elif t is float:
+                key.append((float, v > 0))
+                rt.append(v)
+            elif t is bool:
+                key.append((bool,))
+                rt.append(int(v))
+            elif torch and isinstance(v, tt):
+                if not v.is_cuda:
+                    return None
+                ptr = v.data_ptr()
+                es = v.element_size()
+                if v.is_contiguous():
+                    last = v.numel() - 1
+                else:
+                    last = _last_index(v)
+                key.append((v.dtype, ptr & 15 == 0, _span_class((last + 1) * es, last)))
+                rt.append(ptr)
+            elif t is T.Tensor:
+                ptr = v.ptr
+                last = _last_index(v)
+                key.append((v.dtype.name, ptr & 15 == 0,
+                            _span_class((last + 1) * v.itemsize, last)))
+                rt.append(ptr)
+            else:
+                return None
+        return tuple(key), rt
+
+    def _fast_launch(self, ent: _FastEntry, rt, args, kwargs, grid, stream):
+        if callable(grid):
+            grid = grid(dict(self._bind(args, kwargs)))
+        grid = tuple(int(g) for g in (grid if isinstance(grid, (tuple, list)) else (grid,)))
+        if not 1 <= len(grid) <= 3:
+            raise ValueError(f"grid must have 1 to 3 dimensions, got {grid}")
+        if grid[0] >= 1 << 31 or any(g > 65535 for g in grid[1:]) or any(g < 0 for g in grid):
+            raise ValueError(f"grid {grid} exceeds the HIP limits (x < 2^31, y, z <= 65535)")
+        gx, gy, gz = (grid + (1, 1))[:3]
+        if gx == 0 or gy == 0 or gz == 0:
+            return ent.lc.ck
+        if _trace._active is not None:
+            return None                 # `enceladus.capture` records the general path
+        try:
+            kb = ent.st.pack(*rt)
+        except (struct.error, OverflowError):
+            return None                 # a float beyond fp32's range: general packing
+        if stream is None:
+            stream = D.current_stream()
+        t = _timing.current()
+        if t is not None:
+            t.launch(stream, ent.fn, (gx, gy, gz), ent.block, kb, len(kb))
+            return ent.lc.ck
+        lib = _hip.load_library()
+        err = _errbuf()
+        if lib.ek_launch(stream or None, ent.fn, gx, gy, gz, ent.block, 1, 1, 0, kb, len(kb),
+                         err, 1024):
+            from enceladus_amd.compiler.errors import HipError
+            raise HipError(f"ek_launch: {err.value.decode(errors='replace')}")
+        return ent.lc.ck
+
     def run(self, *args, grid, num_warps: int = 4, num_stages=None, dot_warps=None,
             dot_backend: str = "auto", stream=None, **kwargs):
+        fk = self._fast_key(args, kwargs, num_warps, dot_warps) if not self.interpret else None
+        if fk is not None:
+            ent = self._fast.get(fk[0])
+            if ent is not None and (not ent.lc.deps or ent.lc.current()):
+                ck = self._fast_launch(ent, fk[1], args, kwargs, grid, stream)
+                if ck is not None:
+                    return ck
         if self.interpret or os.environ.get("ENCELADUS_INTERPRET") == "1":
             raise RuntimeError("ENCELADUS_INTERPRET=1 selects the CPU interpreter, which this "
                                "MI355X backend ships only as test infrastructure (oracle/); "
@@ -381,6 +587,10 @@ class JITFunction:
             raise ValueError(f"grid {grid} exceeds the HIP limits (x < 2^31, y, z <= 65535)")
         values = [vals[n] for n in lc.runtime_names]
         lc(grid, values, stream)
+        if fk is not None and fk[0] not in self._fast:
+            ent = _fast_entry(lc)
+            if ent is not None:
+                self._fast[fk[0]] = ent
         return lc.ck
 
     def warmup(self, *args, num_warps: int = 4, dot_warps=None, grid=None, **kwargs):
@@ -398,8 +608,15 @@ class JITFunction:
         """A report of the compiler's decisions for the specialization these arguments
         select (reference: runtime/jit.py:539): MFMA plans, layout conversions and LDS
         by source line. `full=True` appends the IR and the generated HIP."""
+        from enceladus_amd.compiler import codegen_hip
         from enceladus_amd.compiler import explain as EX
         ck = self.warmup(*args, **kwargs)
+        if ck.gen.report is None:
+            # loaded from the specialization cache: regenerate the emitter's report
+            nw, dw = kwargs.get("num_warps", 4), kwargs.get("dot_warps")
+            fn_ir = self.ir_for(*args, **kwargs)
+            ck.gen.report = codegen_hip.generate(
+                fn_ir, {"dot_warps": tuple(dw) if dw else None, "debug": _debug()}).report
         text = EX.explain(ck, grid)
         if full:
             text += f"\n\n--- IR ---\n{ck.ir}\n--- HIP ---\n{ck.hip}"

@@ -431,7 +431,7 @@ def complete_bindings(bindings: list) -> None:
     hosts = [b for b in bindings if b.host is not None]
     if not hosts:
         return
-    if _async:
+    if _async and all(b.key is not None for b in hosts):
         for b in hosts:
             p = _pending.get(b.key)
             if p is None:
@@ -457,6 +457,68 @@ def _bind_host(a: np.ndarray, n: int) -> Binding:
     if n:
         hip.call("ek_memcpy_h2d", ctypes.c_void_p(dev.ptr), ctypes.c_void_p(start), n, None)
     return Binding(dev.ptr, host=a, dev=dev, key=key)
+
+
+def _host_array(x: Any):
+    """The host ndarray behind a NumPy or CPU-torch argument, or None."""
+    if isinstance(x, np.ndarray):
+        return x
+    if _is_torch(x) and x.device.type != "cuda":
+        return x.detach().numpy()
+    return None
+
+
+def bind_arrays(values: list, writes: set) -> tuple[list, list]:
+    """Binds the array arguments of one launch: (device pointer per array argument in
+    order, bindings). Host arrays whose byte spans overlap (views of one buffer, such as
+    `a[::2]` and `a[1::2]`) share one device copy of the union of their spans, so the
+    kernel sees one memory as the host does and the copy back writes each byte once; other
+    host arrays are copied alone, device arrays pass their pointers."""
+    spans = []
+    for i, v in enumerate(values):
+        a = _host_array(v)
+        if a is not None:
+            n = _span_bytes(a)
+            if n:
+                spans.append((a.__array_interface__["data"][0], n, i, a))
+    groups: dict[int, tuple[int, int]] = {}
+    if len(spans) > 1:
+        spans.sort(key=lambda t: t[0])
+        lo, hi, members = spans[0][0], spans[0][0] + spans[0][1], [spans[0][2]]
+        for start, n, i, _ in spans[1:]:
+            if start < hi:
+                hi = max(hi, start + n)
+                members.append(i)
+            else:
+                if len(members) > 1:
+                    for m in members:
+                        groups[m] = (lo, hi)
+                lo, hi, members = start, start + n, [i]
+        if len(members) > 1:
+            for m in members:
+                groups[m] = (lo, hi)
+    ptrs, bindings = [], []
+    shared: dict[tuple[int, int], Binding] = {}
+    for i, v in enumerate(values):
+        if i in groups:
+            lo, hi = groups[i]
+            b = shared.get((lo, hi))
+            if b is None:
+                flush_pending()
+                region = np.ctypeslib.as_array((ctypes.c_uint8 * (hi - lo)).from_address(lo))
+                b = _bind_host(region, hi - lo)
+                b.key = None                 # settled at the launch, never left pending
+                shared[(lo, hi)] = b
+                bindings.append(b)
+            b.writeback = b.writeback or i in writes
+            a = _host_array(v)
+            ptrs.append(b.ptr + (a.__array_interface__["data"][0] - lo))
+            continue
+        b = bind_array(v)
+        b.writeback = i in writes
+        bindings.append(b)
+        ptrs.append(b.ptr)
+    return ptrs, bindings
 
 
 def bind_array(x: Any) -> Binding:

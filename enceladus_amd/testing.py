@@ -58,16 +58,30 @@ class _Events:
 
 def do_bench(fn, warmup: float = 50, rep: int = 20, return_mode: str = "median",
              stream: int | None = None):
+    """Times `fn` on the GPU in ms. Each sample is the GPU time of the dispatches `fn`
+    launches through this runtime, from the first one's start to the last one's end
+    (`runtime.timing.DispatchTimer`), so host launch latency is excluded; an `fn` that
+    launches nothing through the runtime (a torch op) is timed with events around it."""
+    from enceladus_amd.runtime.timing import DispatchTimer
     fn()
     D.synchronize()
     ev = _Events()
+    timer = DispatchTimer()
     s = D.current_stream() if stream is None else stream
-    first = ev.time(fn, s)
+
+    def sample():
+        with timer:
+            fn()
+        if timer.count:
+            return timer.ms()
+        return ev.time(fn, s)
+
+    first = sample()
     n_warm = max(1, int(warmup / max(first, 1e-3)))
     for _ in range(min(n_warm, 1000)):
         fn()
     D.synchronize()
-    times = [ev.time(fn, s) for _ in range(rep)]
+    times = [sample() for _ in range(rep)]
     if return_mode == "all":
         return times
     if return_mode == "min":

@@ -94,6 +94,16 @@ int ek_event_free(void* event, char* err, size_t errlen);
 int ek_event_record(void* event, void* stream, char* err, size_t errlen);
 int ek_event_elapsed_ms(void* start, void* stop, float* ms, char* err, size_t errlen);
 
+/* ek_launch that also records `start_event` (may be NULL) when the dispatch begins and
+ * `stop_event` (may be NULL) when it ends, so the elapsed time between them is the GPU time
+ * of the dispatches alone, without the host's launch latency. Replaces the GPU timestamps
+ * of a flushed command buffer (fr_stream_flush_timed, reference _C/enceladus_rt.mm:626).
+ * Grid x block must stay below 2^32 threads per dimension. */
+int ek_launch_timed_events(void* stream, void* function, uint32_t gx, uint32_t gy,
+                           uint32_t gz, uint32_t bx, uint32_t by, uint32_t bz,
+                           uint32_t dyn_lds, void* kernarg, size_t kernarg_size,
+                           void* start_event, void* stop_event, char* err, size_t errlen);
+
 /* Launches `function` `reps` times back to back between two events and returns the
  * average milliseconds per launch. */
 int ek_timed_launch(void* stream, void* function, uint32_t gx, uint32_t gy, uint32_t gz,

@@ -48,33 +48,38 @@ def test_keys_normalise_scalars_dtypes_and_defaults():
     assert A._key_value(tl.float16) == A._key_value(np.float16) == A._key_value("float16")
 
 
-def test_saved_winner_must_still_be_a_candidate(tmp_path, monkeypatch):
+def test_logged_winner_must_still_be_a_candidate(tmp_path, monkeypatch):
     monkeypatch.setenv("ENCELADUS_CACHE_DIR", str(tmp_path))
     t = A.autotune(CONFIGS, key=["n"])(_scale)
     x = np.zeros(10, np.float32)
     named = A._named(t.fn, (x, x, 10, 2.0), {})
     key = t._key(named)
-    t.best[key] = CONFIGS[1]
-    t._save()
-    data = json.loads(t._path().read_text())
-    assert data[key]["kwargs"] == {"BLOCK": 256} and data[key]["num_warps"] == 8
+    t.tune_log.put(key, CONFIGS[1], {"Config(BLOCK=256)": 0.01})
+    lines = t.log_path().read_text().splitlines()
+    rec = json.loads(lines[-1])
+    assert rec["key"] == key and rec["config"]["kwargs"] == {"BLOCK": 256}
+    assert rec["config"]["num_warps"] == 8 and rec["timings_ms"]
     fresh = A.autotune(CONFIGS, key=["n"])(_scale)
-    fresh._load()
-    assert fresh._from_saved(key, named) == CONFIGS[1]
+    assert fresh._resolve(named, None) == CONFIGS[1]          # from the log, untuned
     pruned = A.autotune(CONFIGS[:1], key=["n"])(_scale)       # the winner is gone
-    pruned._load()
-    assert pruned._from_saved(key, named) is None
+    assert pruned._resolve(named, lambda k: "tuned") == "tuned"
+    # a later line supersedes an earlier one; a torn line is skipped
+    t.tune_log.put(key, CONFIGS[2], {})
+    with open(t.log_path(), "a") as f:
+        f.write('{"key": "torn", "conf')
+    again = A.autotune(CONFIGS, key=["n"])(_scale)
+    assert again._resolve(named, None) == CONFIGS[2]
 
 
 def test_results_file_depends_on_the_compiler(tmp_path, monkeypatch):
     monkeypatch.setenv("ENCELADUS_CACHE_DIR", str(tmp_path))
     t = A.autotune(CONFIGS, key=["n"])(_scale)
-    p1 = t._path()
+    p1 = t.log_path()
     monkeypatch.setattr(A, "_compiler_hash", lambda: "different")
-    assert t._path() != p1
+    assert t.log_path() != p1
 
 
-def test_concurrent_saves_keep_every_result(tmp_path, monkeypatch):
+def test_concurrent_appends_keep_every_result(tmp_path, monkeypatch):
     monkeypatch.setenv("ENCELADUS_CACHE_DIR", str(tmp_path))
     script = f"""
 import sys; sys.path.insert(0, {ROOT!r}); sys.path.insert(0, {os.path.join(ROOT, 'tests')!r})
@@ -85,14 +90,13 @@ from enceladus_amd.runtime import autotuner as A
 i = int(sys.argv[1])
 t = A.autotune(CONFIGS, key=["n"])(_scale)
 for j in range(20):
-    t.best[f"key{{i}}-{{j}}"] = CONFIGS[j % 3]
-    t._save()
+    t.tune_log.put(f"key{{i}}-{{j}}", CONFIGS[j % 3], {{"x" * 300: 1.0}})
 """
     procs = [subprocess.Popen([sys.executable, "-c", script, str(i)]) for i in range(4)]
     assert all(p.wait(timeout=120) == 0 for p in procs)
     t = A.autotune(CONFIGS, key=["n"])(_scale)
-    data = json.loads(t._path().read_text())
-    assert len(data) == 80
+    assert len(t.tune_log.entries()) == 80
+    assert all(json.loads(ln) for ln in t.log_path().read_text().splitlines())
 
 
 def test_state_helpers_restore_and_zero():
@@ -169,3 +173,48 @@ def test_tuned_matmul_example_matches_torch(tmp_path, monkeypatch):
     torch.cuda.synchronize()
     ref = a.float() @ b.float()
     torch.testing.assert_close(c.float(), ref, rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.gpu
+def test_attention_tuned_example_matches_float64(tmp_path, monkeypatch):
+    """attention_tuned (reference: examples/08_flash_attention.py:106-127) tunes over every
+    attention_configs candidate for the dtype and head dimension and returns the same
+    result as `attention`."""
+    import warnings
+    import torch
+    from examples.flash_attention import attention, attention_tuned
+    from oracle import reference_np as R
+    monkeypatch.setenv("ENCELADUS_CACHE_DIR", str(tmp_path))
+    print("[case] attention_tuned bf16 [1, 2, 256, 128] causal", flush=True)
+    g = torch.Generator().manual_seed(4)
+    q, k, v = (torch.randn(1, 2, 256, 128, generator=g).bfloat16().cuda() for _ in range(3))
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        o = attention_tuned(q, k, v, causal=True)
+    torch.cuda.synchronize()
+    want = R.attention(*(x.float().cpu().numpy() for x in (q, k, v)), True)
+    np.testing.assert_allclose(o.float().cpu().numpy(), want, rtol=2e-2, atol=2e-2)
+    ref = attention(q, k, v, True)
+    torch.testing.assert_close(o.float(), ref.float(), rtol=2e-2, atol=2e-2)
+    with pytest.raises(ValueError, match="head_dim"):
+        attention_tuned(q[..., :96], k[..., :96], v[..., :96])
+
+
+@pytest.mark.gpu
+def test_do_bench_times_dispatches_not_host_latency():
+    """do_bench's samples are the GPU time of the dispatches: a launch preceded by a host
+    sleep of 2 ms still times as the kernel alone."""
+    import time
+    import torch
+    from enceladus_amd.testing import do_bench
+    print("[case] do_bench dispatch timing", flush=True)
+    n = 1 << 20
+    x = torch.randn(n, device="cuda")
+    out = torch.empty_like(x)
+
+    def slow_host():
+        time.sleep(0.002)
+        _scale[(n // 1024,)](x, out, n, 2.0, BLOCK=1024)
+    ms = do_bench(slow_host, warmup=1, rep=5)
+    assert ms < 1.0, ms                 # a 4 MB scale takes microseconds, not the 2 ms sleep
+    torch.testing.assert_close(out, x * 2.0)

@@ -244,3 +244,51 @@ def test_constexprs_that_compare_equal_compile_separately():
         _scaled[(1,)](got, S=s)
         O.run_grid(_scaled, (1,), want, S=s)
         np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.gpu
+def test_warm_path_respecializes_on_argument_classes():
+    """The warm launch path keys on argument classes: a size that is (or is not) a multiple
+    of 16, a scale of either sign, an unaligned view and an int64 size each select their
+    own specialization, and every launch is right."""
+    import torch
+    print("[case] warm-path specialization classes", flush=True)
+
+    @enceladus.jit
+    def axpy(x_ptr, out_ptr, n, a, BLOCK: tl.constexpr):
+        offs = tl.program_id(0) * BLOCK + tl.arange(0, BLOCK)
+        m = offs < n
+        tl.store(out_ptr + offs, tl.load(x_ptr + offs, mask=m) * a + 1.0, mask=m)
+
+    base = torch.randn(5000, device="cuda")
+    for n, a, off in [(4096, 2.0, 0), (4004, 2.0, 0), (4096, -3.0, 0), (4096, 2.0, 1),
+                      (4001, 0.5, 3), (4096, 2.0, 0), (4004, 2.0, 0)]:
+        x = base[off:off + n]
+        out = torch.zeros(n, device="cuda")
+        for _ in range(2):          # the second launch takes the warm path
+            axpy[(enceladus.cdiv(n, 256),)](x, out, n, a, BLOCK=256)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(out, x * a + 1.0)
+    keys = list(axpy._fast)
+    assert len(keys) >= 5
+
+
+@pytest.mark.gpu
+def test_interleaved_host_views_written_by_one_launch():
+    """Two written NumPy views of one array whose byte spans overlap (a[::2], a[1::2]) share
+    one device copy: neither copy-back undoes the other's results."""
+    print("[case] interleaved host views", flush=True)
+
+    @enceladus.jit
+    def two_writes(x_ptr, e_ptr, o_ptr, n, BLOCK: tl.constexpr):
+        offs = tl.arange(0, BLOCK)
+        m = offs < n
+        x = tl.load(x_ptr + offs, mask=m)
+        tl.store(e_ptr + offs * 2, x + 1.0, mask=m)
+        tl.store(o_ptr + offs * 2, x + 2.0, mask=m)
+
+    x = np.arange(100, dtype=np.float32)
+    a = np.full(200, -5.0, np.float32)
+    two_writes[(1,)](x, a[::2], a[1::2], 100, BLOCK=128)
+    np.testing.assert_array_equal(a[::2], x + 1.0)
+    np.testing.assert_array_equal(a[1::2], x + 2.0)
