@@ -513,6 +513,11 @@ class Emitter:
         if self.opt.get("no_fusion"):
             return False
         us = self.uses.get(op.result.id, [])
+        if len(us) == 1 and us[0].name == "store" and us[0].operands[1] is op.result and \
+                op.result not in us[0].operands[2:] and not self.opt.get("no_store_fusion"):
+            # the value of a store: computed vector by vector inside the store loop, so
+            # each vector's writes go out while the next one's math runs
+            return True
         if not us or any(u.name not in self._EW_OPS for u in us):
             return False
         if len(us) == 1:
@@ -641,6 +646,13 @@ class Emitter:
                 # signed 32/64-bit math wraps (two's complement), as the language defines
                 # it; C++ leaves signed overflow undefined
                 e = f"ek::w{k}({a}, {b})"
+            elif k == "div" and dt.is_floating() and self._uniform_divisor(op):
+                # relaxed math (the language's default, as Metal's relaxed mode): a tile
+                # divided by a value repeated along it (a broadcast row statistic) is
+                # multiplied by the divisor's reciprocal, one IEEE division per distinct
+                # divisor (the compiler shares `1.0f / b` across the elements that read
+                # the same b); within 1.5 ulp of the quotient
+                e = f"({a} * (1.0f / {b}))"
             elif k in ("add", "sub", "mul", "div"):
                 e = f"({a} {_INFIX[k]} {b})"
             elif k in ("and", "or", "xor"):
@@ -705,6 +717,18 @@ class Emitter:
         if n == "ptr_add":
             return f"({xs[0]} + {xs[1]})"
         raise CompilationError(f"not an elementwise op: {n}")
+
+    def _uniform_divisor(self, op: ir.Op) -> bool:
+        """Whether `op` (a float division) divides a tile by a tile that repeats one value
+        along a dimension (a broadcast row statistic). A scalar divisor keeps the IEEE
+        division: on a row kernel (softmax, one row per program) it measured faster than the
+        reciprocal."""
+        if self.opt.get("math_mode") == "precise" or not op.result.type.shape:
+            return False
+        d = op.operands[1]
+        if not d.type.shape or self.kind.get(d.id) == "scalar":
+            return False
+        return d.op is not None and d.op.name in ("splat", "broadcast")
 
     def cheap(self, v: ir.Value, coords: list[str]) -> str:
         k = self.kind.get(v.id)
@@ -1297,7 +1321,7 @@ class Emitter:
             self.emit(f"if ({cond}) *{self.name[ptr.id]} = {self.name[val.id]};")
             return
         lay = self.mem_layout(ptr)
-        if self._anch(val) and self.kind[val.id] == "anchored":
+        if self._anch(val) and self.kind[val.id] in ("anchored", "fused"):
             vl = self.lay[val.id]
             want = self.mem_vec(ptr, lay)
             # keep the value where it is when that stores as wide a vector, or when each
@@ -1308,9 +1332,24 @@ class Emitter:
                 lay = vl
         V = self.mem_vec(ptr, lay)
         own = self.owner_cond(lay)
-        self.prime((ptr, lay), (mask, lay))
+        self.prime((ptr, lay), (mask, lay), (val, lay))
         pe = lambda i: self.elem(ptr, lay, f"rv + {i}" if i else "rv")  # noqa: E731
-        vals = self.array(val, lay)
+        if self.kind.get(val.id) == "fused":
+            # computed per vector inside each store loop: `vals` names the vector's
+            # temporary, indexed from the vector's first element
+            vals, base = self.fresh("sv"), "0"
+
+            def open_vec():
+                self.emit(f"  {t} {vals}[{V}];")
+                for i in range(V):
+                    self.emit(f"  {vals}[{i}] = "
+                              f"{self.elem(val, lay, f'rv + {i}' if i else 'rv')};")
+        else:
+            vals, base = self.array(val, lay), "rv"
+
+            def open_vec():
+                pass
+        at = lambda i: f"{vals}[{base} + {i}]" if i else f"{vals}[{base}]"  # noqa: E731
         if own:
             self.emit(f"if ({own}) {{")
         st = "vstore" if self.opt.get("no_nt_stores") else "vstore_nt"
@@ -1321,24 +1360,27 @@ class Emitter:
             # edge versioning, as for loads
             self.emit(f"if ({cond}) {{")
             self.emit("#pragma unroll")
-            self.emit(f"for (int rv = 0; rv < {lay.nregs}; rv += {V}) "
-                      f"ek::{st}<{t}, {V}>({pe(0)}, &{vals}[rv]);")
+            self.emit(f"for (int rv = 0; rv < {lay.nregs}; rv += {V}) {{")
+            open_vec()
+            self.emit(f"  ek::{st}<{t}, {V}>({pe(0)}, &{at(0)});")
+            self.emit("}")
             self.emit("} else {")
         self.emit("#pragma unroll")
         self.emit(f"for (int rv = 0; rv < {lay.nregs}; rv += {V}) {{")
+        open_vec()
         if mask is None:
-            self.emit(f"  ek::{st}<{t}, {V}>({pe(0)}, &{vals}[rv]);")
+            self.emit(f"  ek::{st}<{t}, {V}>({pe(0)}, &{at(0)});")
         else:
             me = lambda i: self.elem(mask, lay, f"rv + {i}" if i else "rv")  # noqa: E731
             if V > 1:
                 allm = " && ".join(f"({me(i)})" for i in range(V))
-                self.emit(f"  if ({allm}) {{ ek::{st}<{t}, {V}>({pe(0)}, &{vals}[rv]); }}")
+                self.emit(f"  if ({allm}) {{ ek::{st}<{t}, {V}>({pe(0)}, &{at(0)}); }}")
                 self.emit("  else {")
                 for i in range(V):
-                    self.emit(f"    if ({me(i)}) *({pe(i)}) = {vals}[rv + {i}];")
+                    self.emit(f"    if ({me(i)}) *({pe(i)}) = {at(i)};")
                 self.emit("  }")
             else:
-                self.emit(f"  if ({me(0)}) *({pe(0)}) = {vals}[rv];")
+                self.emit(f"  if ({me(0)}) *({pe(0)}) = {at(0)};")
         self.emit("}")
         if cond:
             self.emit("}")
