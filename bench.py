@@ -23,8 +23,11 @@ core) on a random sample of each grid's programs, and NumPy's closed form (the e
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME[,NAME]]
                        [--no-cpu-baseline]
-NAME is a workload of examples/workloads.py, copy_calib (the counter calibration copy) or
-launch_overhead (host cost of warm launches; part of the default run).
+                       [--pin NAME=INDEX[,...]]
+NAME is a workload of examples/workloads.py, copy_calib (the counter calibration copy),
+torch_matmul / torch_sdpa_causal / torch_sdpa_noncausal (the vendor libraries on the same
+inputs; part of the default run) or launch_overhead (host cost of warm launches; part of
+the default run).
 """
 
 from __future__ import annotations
@@ -101,6 +104,7 @@ def make_launch(jfn, grid, args, options):
             if rc:
                 raise RuntimeError(err.value.decode())
     launch.ck = lc.ck
+    launch.shapes = [[list(g), blk] for _, g, blk, _, _ in disp]
     return launch
 
 
@@ -117,14 +121,19 @@ def rotation_sets(torch, wl, base):
     return sets
 
 
-def measure(torch, timer, wl, steps, warmup):
+def measure(torch, timer, wl, steps, warmup, pin=None):
+    """Times workload `wl`: the autotuner's pick, the fastest listed variant, or, with
+    `pin`, the variant at that index of the workload's table (for profiling runs)."""
     from examples import workloads as W
     host = wl.inputs()
     base = W.device_buffers(wl, host)
     sets = rotation_sets(torch, wl, base)
     r = {"name": wl.name, "bound": wl.bound, "dtype": wl.dtype, "tested_by":
          "tests/test_gpu_bench_configs.py"}
-    if wl.tuned is not None:
+    if pin is not None:
+        r["selected_by"] = "pinned (--pin)"
+        choices = [wl.variants[pin]]
+    elif wl.tuned is not None:
         # the library's autotuner picks the variant (on the seeded inputs)
         tuned = wl.tuned()
         _, args = wl.args(base, wl.variants[0])
@@ -155,10 +164,10 @@ def measure(torch, timer, wl, steps, warmup):
         ms = timer.run(launches, k, max(2, warmup // 2))
         log(f"    {v.label}: {ms * 1e3:.1f} us")
         if best is None or ms < best[0]:
-            best = (ms, v, launches[0].ck.name)
-    ms, v, kname = best
+            best = (ms, v, launches[0].ck.name, launches[0].shapes)
+    ms, v, kname, shapes = best
     r.update({"config": f"{wl.describe} {v.label}", "variant": v.label, "ms": ms,
-              "kernel": kname})
+              "kernel": kname, "dispatches": shapes})
     if wl.bound == "hbm":
         r["bytes"] = wl.work
         r["gbps"] = wl.work / ms / 1e6
@@ -183,6 +192,40 @@ def copy_calibration(torch, timer, steps):
     return {"name": "copy_calib", "config": "torch copy 256 MiB -> 256 MiB", "ms": ms,
             "bytes": 8 * n, "gbps": 8 * n / ms / 1e6, "bound": "hbm", "dtype": "fp32",
             "kernel": "copy", "roofline_frac": 8 * n / ms / 1e6 * 1e9 / HBM_PEAK}
+
+
+TORCH_ROWS = ("torch_matmul", "torch_sdpa_causal", "torch_sdpa_noncausal")
+
+
+def torch_reference(torch, timer, name, steps):
+    """The vendor-library figure for an MFMA workload, on the same inputs and clock
+    conditions: torch.matmul (hipBLASLt) for the fp16 4096^3 product, and torch's
+    scaled_dot_product_attention restricted to its flash backend (an error, never the
+    math fallback, when that backend is missing) for the two attention configs."""
+    from examples import workloads as W
+    if name == "torch_matmul":
+        wl = W.table()["matmul"]
+        b = W.device_buffers(wl)
+        a, bb, c = b["a"], b["b"], b["c"]
+        fn = lambda: torch.matmul(a, bb, out=c)  # noqa: E731
+        cfg, work = "torch.matmul fp16 4096^3 (hipBLASLt)", wl.work
+    else:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        causal = name.endswith("_causal")
+        wl = W.table()["attention_causal" if causal else "attention_noncausal"]
+        b = W.device_buffers(wl)
+        q, k, v = b["q"], b["k"], b["v"]
+
+        def fn():
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+                torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=causal)
+        cfg, work = f"torch SDPA flash backend {wl.describe}", wl.work
+    fn()
+    torch.cuda.synchronize()
+    ms = timer.run([fn], max(5, steps // 2), 3)
+    return {"name": name, "config": cfg, "ms": ms, "flop": work, "bound": "mfma",
+            "tflops": work / ms / 1e9, "roofline_frac": work / ms / 1e9 * 1e12 / MFMA_PEAK_F16,
+            "dtype": wl.dtype, "kernel": "vendor library"}
 
 
 def launch_overhead(torch, reps=5, n_launch=10_000):
@@ -419,7 +462,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default="")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--pin", default="", help="NAME=INDEX[,NAME=INDEX]: time only that "
+                    "variant of the workload's table (profiling runs)")
     args = ap.parse_args()
+    pins = {k: int(v) for k, v in (p.split("=") for p in args.pin.split(",") if p)}
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; multi-GPU runs are out "
                           "of scope (every config shards with no exchange between GPUs)"}))
@@ -431,7 +477,7 @@ def main():
     log(f"device: {info.name.decode()} {info.arch.decode()} CUs={info.compute_units}")
     timer = Timer(torch)
     table = W.table()
-    names = args.only.split(",") if args.only else list(table)
+    names = args.only.split(",") if args.only else list(table) + list(TORCH_ROWS)
     results = {}
     cpu = {}
     for n in names:
@@ -442,7 +488,12 @@ def main():
             results[n] = copy_calibration(torch, timer, args.steps)
             log(f"[bench] copy_calib: {results[n]['gbps']:.0f} GB/s")
             continue
-        r, host = measure(torch, timer, table[n], args.steps, args.warmup)
+        if n in TORCH_ROWS:
+            results[n] = torch_reference(torch, timer, n, args.steps)
+            log(f"[bench] {n}: {results[n]['ms'] * 1e3:.1f} us  "
+                f"{results[n]['tflops']:.1f} TFLOP/s")
+            continue
+        r, host = measure(torch, timer, table[n], args.steps, args.warmup, pins.get(n))
         results[n] = r
         log(f"[bench] {n}: {r['ms'] * 1e3:.1f} us  " +
             (f"{r['gbps']:.0f} GB/s" if "gbps" in r else f"{r['tflops']:.1f} TFLOP/s") +
@@ -460,7 +511,8 @@ def main():
         print(json.dumps({"metric": "warm launch overhead (us per launch)",
                           "launch_overhead": launch_overhead(torch)}), flush=True)
         return
-    real = {k: r for k, r in results.items() if k != "copy_calib"} or results
+    real = {k: r for k, r in results.items()
+            if k != "copy_calib" and k not in TORCH_ROWS} or results
     head = real.get("softmax") or next(iter(real.values()))
     line = {
         "metric": METRIC,

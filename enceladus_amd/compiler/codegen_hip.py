@@ -720,15 +720,16 @@ class Emitter:
 
     def _uniform_divisor(self, op: ir.Op) -> bool:
         """Whether `op` (a float division) divides a tile by a tile that repeats one value
-        along a dimension (a broadcast row statistic). A scalar divisor keeps the IEEE
-        division: on a row kernel (softmax, one row per program) it measured faster than the
-        reciprocal."""
+        along a dimension (a broadcast row statistic, as attention's `acc / l[:, None]`).
+        A scalar divisor, splat or not, keeps the IEEE division: on a row kernel (softmax,
+        one row per program, the row sum splat over the row) the division measured 4%
+        faster than the reciprocal in interleaved A/B runs on MI355X."""
         if self.opt.get("math_mode") == "precise" or not op.result.type.shape:
             return False
         d = op.operands[1]
         if not d.type.shape or self.kind.get(d.id) == "scalar":
             return False
-        return d.op is not None and d.op.name in ("splat", "broadcast")
+        return d.op is not None and d.op.name == "broadcast"
 
     def cheap(self, v: ir.Value, coords: list[str]) -> str:
         k = self.kind.get(v.id)
