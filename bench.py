@@ -24,7 +24,9 @@ core) on a random sample of each grid's programs, and NumPy's closed form (the e
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME[,NAME]]
                        [--no-cpu-baseline]
                        [--pin NAME=INDEX[,...]]
-NAME is a workload of examples/workloads.py, copy_calib (the counter calibration copy),
+NAME is a workload of examples/workloads.py (the BASELINE configs, and copy_rows /
+copy_flat: plain copies of the same bytes by this backend, the HBM ceiling the row kernels
+are read against), copy_calib (torch's device copy, the counter calibration),
 torch_matmul / torch_sdpa_causal / torch_sdpa_noncausal (the vendor libraries on the same
 inputs; part of the default run) or launch_overhead (host cost of warm launches; part of
 the default run).
@@ -494,11 +496,13 @@ def main():
                 f"{results[n]['tflops']:.1f} TFLOP/s")
             continue
         r, host = measure(torch, timer, table[n], args.steps, args.warmup, pins.get(n))
+        if table[n].ceiling:
+            r["ceiling"] = True
         results[n] = r
         log(f"[bench] {n}: {r['ms'] * 1e3:.1f} us  " +
             (f"{r['gbps']:.0f} GB/s" if "gbps" in r else f"{r['tflops']:.1f} TFLOP/s") +
             f"  ({100 * r['roofline_frac']:.1f}% of roofline)")
-        if not args.no_cpu_baseline:
+        if not args.no_cpu_baseline and not table[n].ceiling:
             v = next(x for x in table[n].variants if x.label == r["variant"])
             cpu[n] = cpu_workload(table[n], host, v)
             r["cpu"] = cpu[n]
@@ -512,7 +516,7 @@ def main():
                           "launch_overhead": launch_overhead(torch)}), flush=True)
         return
     real = {k: r for k, r in results.items()
-            if k != "copy_calib" and k not in TORCH_ROWS} or results
+            if k != "copy_calib" and k not in TORCH_ROWS and not r.get("ceiling")} or results
     head = real.get("softmax") or next(iter(real.values()))
     line = {
         "metric": METRIC,

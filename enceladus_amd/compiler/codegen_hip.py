@@ -719,16 +719,22 @@ class Emitter:
         raise CompilationError(f"not an elementwise op: {n}")
 
     def _uniform_divisor(self, op: ir.Op) -> bool:
-        """Whether `op` (a float division) divides a tile by a tile that repeats one value
-        along a dimension (a broadcast row statistic, as attention's `acc / l[:, None]`).
-        A scalar divisor, splat or not, keeps the IEEE division: on a row kernel (softmax,
-        one row per program, the row sum splat over the row) the division measured 4%
-        faster than the reciprocal in interleaved A/B runs on MI355X."""
-        if self.opt.get("math_mode") == "precise" or not op.result.type.shape:
+        """Whether `op` (a float division) is emitted as a multiplication by the divisor's
+        reciprocal: under relaxed math when the divisor is a tile that repeats one value
+        along a dimension (a broadcast row statistic, as attention's `acc / l[:, None]`);
+        under fast math also for a scalar or splat divisor. Relaxed math keeps the IEEE
+        division for a scalar divisor: on a row kernel (softmax, one row per program, the
+        row sum splat over the row) the division measured 4% faster than the reciprocal in
+        interleaved A/B runs on MI355X. The "precise" setting (an experiment switch of
+        ENCELADUS_CODEGEN) keeps every division."""
+        mode = self.opt.get("math_mode", "relaxed")
+        if mode == "precise" or not op.result.type.shape:
             return False
         d = op.operands[1]
         if not d.type.shape or self.kind.get(d.id) == "scalar":
-            return False
+            return mode == "fast"
+        if d.op is not None and d.op.name == "splat":
+            return mode == "fast"
         return d.op is not None and d.op.name == "broadcast"
 
     def cheap(self, v: ir.Value, coords: list[str]) -> str:

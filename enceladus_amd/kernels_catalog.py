@@ -65,8 +65,10 @@ def _input_shapes(wl) -> dict:
     from examples import workloads as W
     if wl.name == "vector_add":
         return {"x": ((W.VADD_N,), "float32"), "y": ((W.VADD_N,), "float32")}
-    if wl.name in ("softmax",):
+    if wl.name in ("softmax", "copy_rows"):
         return {"x": ((W.ROWS, W.COLS), "float32")}
+    if wl.name == "copy_flat":
+        return {"x": ((W.ROWS * W.COLS,), "float32")}
     if wl.name == "rmsnorm":
         return {"x": ((W.ROWS, W.COLS), "float32"), "w": ((W.COLS,), "float32")}
     if wl.name.startswith("matmul"):

@@ -333,6 +333,12 @@ class Launcher:
                                            (int(rec[2]), int(rec[3]), int(rec[4])))
 
 
+# Float math modes (reference: runtime/jit.py:56). "relaxed" (the default) multiplies by
+# the reciprocal of a broadcast row statistic instead of dividing by it; "fast" does so for
+# every divisor that is uniform along the divided tile, scalars included.
+MATH_MODES = ("relaxed", "fast")
+
+
 class JITFunction:
     """A kernel or device function created by `@enceladus.jit`."""
 
@@ -340,6 +346,8 @@ class JITFunction:
 
     def __init__(self, fn: Callable, do_not_specialize=(), math_mode: str = "relaxed",
                  interpret=None):
+        if math_mode not in MATH_MODES:
+            raise ValueError(f"math_mode must be one of {MATH_MODES}, but got {math_mode!r}")
         self.fn = fn
         self.__name__ = fn.__name__
         self.__doc__ = fn.__doc__
@@ -427,7 +435,8 @@ class JITFunction:
                 tuple(dot_warps) if dot_warps else None)
 
     def _compile_for(self, types, facts, consts, num_warps, dot_warps) -> Launcher:
-        options = {"dot_warps": tuple(dot_warps) if dot_warps else None}
+        options = {"dot_warps": tuple(dot_warps) if dot_warps else None,
+                   "math_mode": self.math_mode}
         # ENCELADUS_CODEGEN="flag,flag=value": emitter switches for experiments (e.g.
         # no_staging, no_gemm_template, coarsen); part of the specialization key below.
         for item in filter(None, os.environ.get("ENCELADUS_CODEGEN", "").split(",")):

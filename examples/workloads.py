@@ -19,6 +19,9 @@ from typing import Callable
 
 import numpy as np
 
+import enceladus
+import enceladus.language as tl
+
 
 @dataclass(frozen=True)
 class Variant:
@@ -66,6 +69,7 @@ class Workload:
     variants: list = field(default_factory=list)
     tuned: Callable[[], object] | None = None  # the autotuned kernel, when autotuned
     fixed: dict = field(default_factory=dict)  # constexprs the autotuned launch passes
+    ceiling: bool = False                 # a copy kernel that calibrates the HBM rows
 
     def variant_of(self, config) -> Variant:
         """The variant an autotuner `Config` selects for this workload."""
@@ -220,6 +224,38 @@ def _scan_args(b, v):
     return (m,), (b["out"], b["x"], m, n, n, n)
 
 
+# -- copy ceilings ----------------------------------------------------------------------
+# Plain copies compiled by this backend, in the row kernels' shape (one program per 32 KB
+# row) and flat (small tiles, many programs): the HBM rate a kernel with the same access
+# pattern and no arithmetic reaches on the same box. Not BASELINE configs.
+
+@enceladus.jit
+def copy_rows_kernel(out_ptr, in_ptr, stride, n_cols, BLOCK: tl.constexpr):
+    row = tl.program_id(0)
+    cols = tl.arange(0, BLOCK)
+    mask = cols < n_cols
+    x = tl.load(in_ptr + row * stride + cols, mask=mask)
+    tl.store(out_ptr + row * stride + cols, x, mask=mask)
+
+
+@enceladus.jit
+def copy_flat_kernel(out_ptr, in_ptr, n, BLOCK: tl.constexpr):
+    offs = tl.program_id(0) * BLOCK + tl.arange(0, BLOCK)
+    mask = offs < n
+    tl.store(out_ptr + offs, tl.load(in_ptr + offs, mask=mask), mask=mask)
+
+
+def _copy_rows_args(b, v):
+    m, n = b["x"].shape
+    return (m,), (b["out"], b["x"], n, n)
+
+
+def _copy_flat_args(b, v):
+    n = b["x"].numel()
+    block = dict(v.constexprs)["BLOCK"]
+    return ((n + block - 1) // block,), (b["out"], b["x"], n)
+
+
 def _k(module, name):
     def get():
         import importlib
@@ -270,6 +306,16 @@ def table() -> dict[str, Workload]:
         {"out": ((SCAN_ROWS, SCAN_COLS), "int32")}, _scan_args,
         [Variant((("BLOCK_M", 1), ("BLOCK_N", SCAN_COLS), ("REVERSE", False)), nw)
          for nw in HBM_WARPS])
+    w["copy_rows"] = Workload(
+        "copy_rows", "fp32 [4096, 8192] one row per program", lambda: copy_rows_kernel,
+        "hbm", ROWS * COLS * 8, "fp32", _row_inputs, {"out": ((ROWS, COLS), "float32")},
+        _copy_rows_args, [Variant((("BLOCK", 8192),), nw) for nw in HBM_WARPS],
+        ceiling=True)
+    w["copy_flat"] = Workload(
+        "copy_flat", "fp32 2^25 elements", lambda: copy_flat_kernel, "hbm",
+        ROWS * COLS * 8, "fp32", lambda: {"x": _f32(0, ROWS * COLS)},
+        {"out": ((ROWS * COLS,), "float32")}, _copy_flat_args,
+        [Variant((("BLOCK", b),), 4) for b in (1024, 2048, 4096)], ceiling=True)
     return w
 
 

@@ -322,3 +322,27 @@ def test_softmax_scale_fold():
     assert not any(op.name == "fma" for op in neg)
     red = [op for op in neg if op.name == "reduce" and op.attrs["kind"] == "max"][0]
     assert red.operands[0].op.operands[1].op.name == "binary"
+
+
+def test_math_modes_pick_division_or_reciprocal():
+    """relaxed (the default): a tile divided by a broadcast row statistic multiplies by its
+    reciprocal, a scalar divisor keeps the IEEE division; fast: both multiply; an unknown
+    mode is refused (reference: runtime/jit.py:56, :234-235)."""
+    def src(mode, divisor_is_row):
+        @enceladus.jit(math_mode=mode)
+        def k(x_ptr, o_ptr, s, BLOCK: tl.constexpr):
+            r = tl.arange(0, BLOCK)
+            x = tl.load(x_ptr + r[:, None] * BLOCK + r[None, :])
+            if divisor_is_row:
+                y = x / tl.sum(x, 1)[:, None]
+            else:
+                y = x / s
+            tl.store(o_ptr + r[:, None] * BLOCK + r[None, :], y)
+        x = np.zeros(4, np.float32)
+        f = k.ir_for(x, x, 2.0, BLOCK=32)
+        return codegen_hip.generate(f, {"math_mode": mode}).source
+    assert "(1.0f / " in src("relaxed", True)
+    assert "(1.0f / " not in src("relaxed", False)
+    assert "(1.0f / " in src("fast", False)
+    with pytest.raises(ValueError, match="math_mode"):
+        enceladus.jit(math_mode="precise")(lambda x: x)

@@ -16,7 +16,8 @@ against the CPU oracle (reference protocol: tests/conftest.py:102-145):
   programs;
 - flash attention bf16 [4,32,4096,128] causal and [4,32,1024,128]: the oracle on a sample of
   (start_m, batch*head) programs stratified over start_m (first, middle, last blocks) and
-  the float64 closed form on the same rows.
+  the float64 closed form on the same rows;
+- the two copy kernels the benchmark reports as HBM ceilings: bit-exact.
 
 Tolerances: the reference's by output dtype (tests/conftest.py:75-79): fp32 (1e-5, 1e-5)
 with atol 1e-8 for softmax outputs of ~1/8192; fp16 (atol 1e-3, rtol 2e-3); bf16
@@ -146,6 +147,16 @@ def test_vector_add_full(v):
     for p in pids:
         s = slice(p * 1024, (p + 1) * 1024)
         assert np.array_equal(got[s], want[s]), f"program {p}"
+
+
+@pytest.mark.parametrize("name,v", [pytest.param(nm, v, id=f"{nm}-" + _id(v))
+                                    for nm in ("copy_rows", "copy_flat")
+                                    for v in TABLE[nm].variants])
+def test_copy_ceilings_full(name, v):
+    """The copy kernels the bench reports as HBM ceilings move every byte unchanged."""
+    _say(f"{name} {v.label}")
+    b, _ = _run(name, v)
+    assert np.array_equal(b["out"].cpu().numpy(), _host(name)["x"])
 
 
 HIST_SIZES = [W.HIST_N, W.HIST_N + 3 * 1024 + 5]
