@@ -527,7 +527,10 @@ def main():
         "vs_baseline": None, "dtype": head.get("dtype", "fp32"), "data": "synthetic",
         "config": {"workload": f"{head['name']} {head['config']}",
                    "device": info.name.decode(), "arch": info.arch.decode(),
-                   "cus": info.compute_units},
+                   "cus": info.compute_units, "max_clock_mhz": info.clock_khz // 1000,
+                   "mem_clock_mhz": info.mem_clock_khz // 1000,
+                   "mem_bus_bits": info.mem_bus_width, "lds_per_block": info.lds_per_block,
+                   "l2_bytes": info.l2_bytes, "hbm_bytes": info.total_mem},
         "roofline": ({"bound": "hbm", "achieved": round(head["gbps"], 1),
                       "peak": HBM_PEAK / 1e9, "unit": "GB/s"} if head["bound"] == "hbm" else
                      {"bound": "mfma", "achieved": round(head["tflops"], 1),
