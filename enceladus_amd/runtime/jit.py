@@ -596,10 +596,16 @@ class JITFunction:
             raise ValueError(f"grid {grid} exceeds the HIP limits (x < 2^31, y, z <= 65535)")
         values = [vals[n] for n in lc.runtime_names]
         lc(grid, values, stream)
-        if fk is not None and fk[0] not in self._fast:
-            ent = _fast_entry(lc)
-            if ent is not None:
-                self._fast[fk[0]] = ent
+        if fk is not None:
+            cur = self._fast.get(fk[0])
+            if cur is None or cur.lc is not lc:
+                # first launch of this key, or a recompile after a global the kernel reads
+                # changed: the warm entry follows the launcher now in use
+                ent = _fast_entry(lc)
+                if ent is not None:
+                    self._fast[fk[0]] = ent
+                else:
+                    self._fast.pop(fk[0], None)
         return lc.ck
 
     def warmup(self, *args, num_warps: int = 4, dot_warps=None, grid=None, **kwargs):

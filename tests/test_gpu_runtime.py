@@ -273,6 +273,39 @@ def test_warm_path_respecializes_on_argument_classes():
     assert len(keys) >= 5
 
 
+WARM_SCALE = 2.0
+
+
+@pytest.mark.gpu
+def test_warm_path_follows_a_changed_global():
+    """A global the kernel reads changes between warm launches: the next launch recompiles,
+    and the warm entry then follows the new code (reference: runtime/jit.py:1037-1234)."""
+    import torch
+    global WARM_SCALE
+    print("[case] warm path after a global changes", flush=True)
+
+    @enceladus.jit
+    def scale(x_ptr, out_ptr, n, BLOCK: tl.constexpr):
+        offs = tl.program_id(0) * BLOCK + tl.arange(0, BLOCK)
+        m = offs < n
+        tl.store(out_ptr + offs, tl.load(x_ptr + offs, mask=m) * WARM_SCALE, mask=m)
+
+    x = torch.randn(1000, device="cuda")
+    out = torch.zeros_like(x)
+    try:
+        for want in (2.0, 5.0, -1.5):
+            WARM_SCALE = want
+            for _ in range(3):      # the general path once, then warm launches
+                out.zero_()
+                scale[(4,)](x, out, 1000, BLOCK=256)
+                torch.cuda.synchronize()
+                torch.testing.assert_close(out, x * want)
+            (ent,) = scale._fast.values()
+            assert ent.lc.current()
+    finally:
+        WARM_SCALE = 2.0
+
+
 @pytest.mark.gpu
 def test_interleaved_host_views_written_by_one_launch():
     """Two written NumPy views of one array whose byte spans overlap (a[::2], a[1::2]) share
