@@ -255,3 +255,36 @@ def test_vector_accesses_match_scalar_ones(dtype, case, m, n, sx, off):
     want = torch.zeros((m, 64), dtype=td)
     want[:, :n] = x.cpu()[:, :n] * 2 + 1
     assert torch.equal(y.cpu(), want)
+
+
+@pytest.mark.parametrize("mode", ["relaxed", "fast"])
+def test_math_mode_divisions_stay_within_their_bound(mode):
+    """A tile divided by its row sums (broadcast) and by a scalar: IEEE division where the
+    mode keeps it (bit-exact against NumPy's float32 quotient), a reciprocal multiply where
+    it does not (within 1.5 ulp of the quotient; reference math modes: runtime/jit.py:56)."""
+    print(f"[case] math_mode={mode} divisions", flush=True)
+
+    @enceladus.jit(math_mode=mode)
+    def div(x_ptr, r_ptr, s_ptr, d, BLOCK: tl.constexpr):
+        rows = tl.arange(0, BLOCK)[:, None]
+        cols = tl.arange(0, BLOCK)[None, :]
+        x = tl.load(x_ptr + rows * BLOCK + cols)
+        tl.store(r_ptr + rows * BLOCK + cols, x / tl.sum(x, 1)[:, None])
+        tl.store(s_ptr + rows * BLOCK + cols, x / d)
+
+    rng = np.random.default_rng(3)
+    x = rng.uniform(0.5, 2.0, (32, 32)).astype(np.float32)
+    r = np.zeros_like(x)
+    s = np.zeros_like(x)
+    d = np.float32(3.7)
+    div[(1,)](x, r, s, float(d), BLOCK=32)
+    rowsum = x.astype(np.float64).sum(1, keepdims=True)
+    q_row = (x / rowsum).astype(np.float32)
+    ulp = np.spacing(np.abs(q_row))
+    # the device's fp32 row sum may differ from float64's by its own rounding
+    assert np.all(np.abs(r - q_row) <= 1.5 * ulp + 2e-6 * np.abs(q_row))
+    q_s = x / d
+    if mode == "relaxed":
+        np.testing.assert_array_equal(s, q_s)
+    else:
+        assert np.all(np.abs(s - q_s) <= 1.5 * np.spacing(np.abs(q_s)))
