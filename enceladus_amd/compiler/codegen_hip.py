@@ -2268,6 +2268,22 @@ class Emitter:
             self.emit("#pragma unroll")
             self.emit(f"for (int r = 0; r < {lc.nregs}; ++r) {nm}[r] = ek::f32({e});")
         tm, tn, tk, kpl = plan.tm, plan.tn, plan.tk, ins.kpl
+        dd = getattr(self, "deferred_dma", None)
+        copies = {}
+        if (sa or sb) and dd is not None and not dd["used"] and tk > 1:
+            # The loop's stage copies go out from this dot, spread over its k steps: copy c
+            # after the MFMAs of step c * (tk - 1) // n, so each step's copy issue overlaps
+            # the MFMAs already queued instead of stalling the wave in one block (the first
+            # fragment reads still go out before any copy).
+            dd["used"] = True
+            if self.opt.get("dma_block"):
+                copies = {0: dd["chunks"]}
+            else:
+                n = len(dd["chunks"])
+                for c_, ln in enumerate(dd["chunks"]):
+                    copies.setdefault(c_ * (tk - 1) // n, []).append(ln)
+            for ln in dd["setup"]:
+                self.emit(ln)
         # Per k step: read every A and B fragment first (staged operands come from LDS),
         # then issue the TM x TN MFMAs, so LDS latency overlaps the previous step's MFMAs.
         self.emit("#pragma unroll")
@@ -2299,12 +2315,9 @@ class Emitter:
         self.emit("    #pragma unroll")
         self.emit(f"    for (int in_ = 0; in_ < {tn}; ++in_) "
                   f"ek::{ins.fn}(&{nm}[(im * {tn} + in_) * {nacc}], {x}, {y});")
-        dd = getattr(self, "deferred_dma", None)
-        if (sa or sb) and dd is not None and not dd["used"] and tk > 1:
-            # the loop's stage copies, after this dot's first k slice
-            dd["used"] = True
-            self.emit("  if (kk == 0) {")
-            for ln in dd["lines"]:
+        for k_, lns in sorted(copies.items()):
+            self.emit(f"  if (kk == {k_}) {{")
+            for ln in lns:
                 self.emit("    " + ln)
             self.emit("  }")
         self.emit("}")
@@ -2558,35 +2571,42 @@ class Emitter:
         _STAGE_LAYOUTS[key] = (sl, best[0][0], LDS.ideal(acc))
         return sl
 
-    def _stage_dma(self, info, kval: str, stage: str) -> list[str]:
-        """Copies the tile at row origin `kval` (or the loop-invariant one) into stage `stage`.
-        Rows outside [0, shape0) fall past the buffer resource and arrive as zeros."""
+    def _stage_dma_parts(self, info, kval: str, stage: str) -> tuple[list[str], list[str]]:
+        """Copies the tile at row origin `kval` (or the loop-invariant one) into stage `stage`,
+        as (set-up lines, one line per 16-byte copy of this thread) so that the copies can be
+        spread over a dot's k steps. Rows outside [0, shape0) fall past the buffer resource
+        and arrive as zeros."""
         d = info["desc"]
         o0, _ = self._stage_offsets(info, kval)
         idx = info["smem"][len("ek_stg"):]
         R, per = info["R"], info["per"]
         base, s0, sh0 = d["base"], d["strides"][0], d["shape"][0]
+        t = self.fresh("cp")
         # A tile starting at row >= 0 (the usual case) copies through a resource based at its
-        # first row, so the per-chunk offsets are loop-invariant; otherwise rows before 0
-        # need the general form with the row offset in each lane's address.
-        return ["{", f"  const int ek_r0 = {o0};",
-                f"  const uint32_t ek_ls = ek_dml{idx} + (uint32_t)({stage}) * "
-                f"{info['stage_elems'] * 2}u;",
-                "  if (ek_r0 >= 0) {",
-                f"    const ek::i32x4 ek_rs = ek::rsrc_words({base} + (int64_t)ek_r0 * {s0}, "
-                f"ek_r0 < {sh0} ? (uint32_t)({sh0} - ek_r0) * (uint32_t){s0} * 2u : 0u);",
-                "    #pragma unroll",
-                f"    for (int i = 0; i < {per}; ++i) ek::dma16(ek_rs, ek_ls + i * {self.nt * 16}, "
-                f"ek_dmb{idx}[i]);",
-                "  } else {",
-                f"    const ek::i32x4 ek_rs = ek::rsrc_words({base}, ek_r0 > -{R} ? "
-                f"(uint32_t){sh0} * (uint32_t){s0} * 2u : 0u);",
-                f"    const int ek_rb = ek_r0 * {s0};",
-                "    #pragma unroll",
-                f"    for (int i = 0; i < {per}; ++i) ek::dma16(ek_rs, ek_ls + i * {self.nt * 16}, "
-                f"ek_dmo{idx}[i] >= 0 ? (ek_rb + ek_dmo{idx}[i]) * 2 : ek::kOOB);",
-                "  }",
-                "}"]
+        # first row, so the per-chunk offsets are the loop-invariant ones; otherwise rows
+        # before 0 need the general form with the row offset in each lane's address. The
+        # choice is uniform, made with selects so the copies need no branch.
+        setup = [f"const int {t}_r0 = {o0};",
+                 f"const uint32_t {t}_ls = ek_dml{idx} + (uint32_t)({stage}) * "
+                 f"{info['stage_elems'] * 2}u;",
+                 f"const bool {t}_pos = {t}_r0 >= 0;",
+                 f"const ek::i32x4 {t}_rs = {t}_pos ? ek::rsrc_words({base} + (int64_t){t}_r0 * "
+                 f"{s0}, {t}_r0 < {sh0} ? (uint32_t)({sh0} - {t}_r0) * (uint32_t){s0} * 2u : 0u) "
+                 f": ek::rsrc_words({base}, {t}_r0 > -{R} ? (uint32_t){sh0} * (uint32_t){s0} * 2u "
+                 ": 0u);",
+                 f"const int {t}_rb = {t}_r0 * {s0};",
+                 f"int {t}_of[{per}];",
+                 "#pragma unroll",
+                 f"for (int i = 0; i < {per}; ++i) {t}_of[i] = {t}_pos ? ek_dmb{idx}[i] : "
+                 f"(ek_dmo{idx}[i] >= 0 ? ({t}_rb + ek_dmo{idx}[i]) * 2 : ek::kOOB);"]
+        chunks = [f"ek::dma16({t}_rs, {t}_ls + {i * self.nt * 16}u, {t}_of[{i}]);"
+                  for i in range(per)]
+        return setup, chunks
+
+    def _stage_dma(self, info, kval: str, stage: str) -> list[str]:
+        """The whole copy of one tile as a block (loop prologues)."""
+        setup, chunks = self._stage_dma_parts(info, kval, stage)
+        return ["{"] + ["  " + ln for ln in setup + chunks] + ["}"]
 
     def _stage_setup(self, info, idx: int):
         ld = info["op"]
@@ -2985,10 +3005,13 @@ class Emitter:
             # everyone's are, so the previous stage can be refilled.
             self.emit(f'asm volatile("s_waitcnt vmcnt({(nst - 2) * dcount}) lgkmcnt(0)\\n\\t'
                       f's_barrier" ::: "memory");')
-            lines = []
+            setup, chunks = [], []
             for info in stg:
-                lines += self._stage_dma(info, f"({ivn} + {nst - 1} * {step})",
-                                         f"(ek_it{li} + {nst - 1}) % {nst}")
+                su, ch = self._stage_dma_parts(info, f"({ivn} + {nst - 1} * {step})",
+                                               f"(ek_it{li} + {nst - 1}) % {nst}")
+                setup += su
+                chunks += ch
+            lines = ["{"] + ["  " + ln for ln in setup + chunks] + ["}"]
             # The copies for a later stage may go anywhere after the barrier: the first dot
             # that reads a stage issues them after its first k slice (its fragment reads go
             # out first and hide behind the copy issue); otherwise they land here.
@@ -2996,7 +3019,7 @@ class Emitter:
             self.cur.items.append(slot)
             prev_dma = getattr(self, "deferred_dma", None)
             self.deferred_dma = None if self.opt.get("no_late_dma") else \
-                {"lines": lines, "used": False}
+                {"lines": lines, "setup": setup, "chunks": chunks, "used": False}
             if self.deferred_dma is None:
                 slot.extend(self.cur.indent + ln for ln in lines)
         elif stg:

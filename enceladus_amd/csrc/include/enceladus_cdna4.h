@@ -829,39 +829,55 @@ struct GemmDma {
     }
   }
 
-  template <int KK0, int KK1>
-  EK_INLINE void compute(float* acc, const uint16_t* st, int lane, int wm, int wn) {
+  // The j-th of this thread's D copies of the k-th tile (j < A_DMA: A, else B).
+  EK_INLINE void copy_one(int j, i32x4 ra, i32x4 rb, int ldb, int K, int k, uint32_t st,
+                          int wave) {
+    if (j < A_DMA) {
+      const int off = (k + BK <= K || k + a_kc[j] + 8 <= K) ? (a_off[j] + k) * 2 : kOOB;
+      dma16(ra, st + (j * NT + wave * 64) * 16, off);
+    } else {
+      const int i = j - A_DMA;
+      const int off = b_off[i] >= 0 ? (b_off[i] + k * ldb) * 2 : kOOB;
+      dma16(rb, st + A_ELEMS * 2 + (i * NT + wave * 64) * 16, off);
+    }
+  }
+
+  // One k slice: every A and B fragment read, then the TM x TN MFMAs.
+  EK_INLINE void compute_kk(int kk, float* acc, const uint16_t* st, int lane, int wm, int wn) {
     typedef short v4s __attribute__((ext_vector_type(4)));
     const u32x4* sA = reinterpret_cast<const u32x4*>(st);
     const uint16_t* sB = st + A_ELEMS;
     const int r32 = lane & 31, h = lane >> 5;
     const int g = lane >> 4, ti = (lane >> 2) & 3, tq = lane & 3;
+    T a[TM][8], b[TN][8];
+    const int kc = kk * 2 + h;
 #pragma unroll
-    for (int kk = KK0; kk < KK1; ++kk) {
-      T a[TM][8], b[TN][8];
-      const int kc = kk * 2 + h;
-#pragma unroll
-      for (int tm = 0; tm < TM; ++tm) {
-        const u32x4 v = sA[a_chunk(wm * (BM / WM) + tm * 32 + r32, kc)];
-        __builtin_memcpy(a[tm], &v, 16);
-      }
-#pragma unroll
-      for (int tn = 0; tn < TN; ++tn) {
-        const int n = wn * (BN / WN) + tn * 32 + 16 * (g & 1) + 4 * tq;
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          const int k = kk * 16 + 8 * (g >> 1) + 4 * half + ti;
-          const uint16_t* src = sB + b_chunk(k, n >> 3) * 8 + (n & 7);
-          const v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) v4s*)(src));
-          __builtin_memcpy(&b[tn][4 * half], &v, 8);
-        }
-      }
-#pragma unroll
-      for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-        for (int tn = 0; tn < TN; ++tn) mfma_32x32x16(&acc[(tm * TN + tn) * 16], a[tm], b[tn]);
+    for (int tm = 0; tm < TM; ++tm) {
+      const u32x4 v = sA[a_chunk(wm * (BM / WM) + tm * 32 + r32, kc)];
+      __builtin_memcpy(a[tm], &v, 16);
     }
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      const int n = wn * (BN / WN) + tn * 32 + 16 * (g & 1) + 4 * tq;
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int k = kk * 16 + 8 * (g >> 1) + 4 * half + ti;
+        const uint16_t* src = sB + b_chunk(k, n >> 3) * 8 + (n & 7);
+        const v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v4s*)(src));
+        __builtin_memcpy(&b[tn][4 * half], &v, 8);
+      }
+    }
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) mfma_32x32x16(&acc[(tm * TN + tn) * 16], a[tm], b[tn]);
+  }
+
+  template <int KK0, int KK1>
+  EK_INLINE void compute(float* acc, const uint16_t* st, int lane, int wm, int wn) {
+#pragma unroll
+    for (int kk = KK0; kk < KK1; ++kk) compute_kk(kk, acc, st, lane, wm, wn);
   }
 
   // Runs the whole k loop: k = lo, lo + BK, ... < hi.
@@ -887,11 +903,27 @@ struct GemmDma {
       // this wave's copies of stage `it` have landed (S - 2 younger stages may still fly),
       // its reads of the previous stage are complete; then everyone's are.
       asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((S - 2) * D) : "memory");
-      // the first k slice's fragment reads go out before the copies, so their latency
-      // hides behind the copy issue instead of stalling the first MFMA
-      compute<0, SPLIT>(acc, s16 + (it % S) * STAGE, lane, wm, wn);
-      copy(ra, rb, ldb, K, lo + (it + S - 1) * BK, l0 + ((it + S - 1) % S) * STAGE * 2, wave);
-      compute<SPLIT, TK>(acc, s16 + (it % S) * STAGE, lane, wm, wn);
+      // The first SPLIT k slices' fragment reads go out before any copy, so their latency
+      // hides behind the copy issue instead of stalling the first MFMA; the copies of the
+      // stage S - 1 ahead are then spread over the remaining slices, a share before each
+      // slice's reads, so each share's issue overlaps the MFMAs already queued (as one block
+      // the copies kept the wave from issuing for 500-800 cycles per k step).
+      const uint16_t* cur = s16 + (it % S) * STAGE;
+      compute<0, SPLIT>(acc, cur, lane, wm, wn);
+      if constexpr (SPLIT < TK) {
+        constexpr int SL = TK - SPLIT, PER = (D + SL - 1) / SL;
+        const int kn = lo + (it + S - 1) * BK;
+        const uint32_t stn = l0 + ((it + S - 1) % S) * STAGE * 2;
+#pragma unroll
+        for (int q = 0; q < SL; ++q) {
+#pragma unroll
+          for (int j = q * PER; j < (q + 1) * PER && j < D; ++j)
+            copy_one(j, ra, rb, ldb, K, kn, stn, wave);
+          compute_kk(SPLIT + q, acc, cur, lane, wm, wn);
+        }
+      } else {
+        copy(ra, rb, ldb, K, lo + (it + S - 1) * BK, l0 + ((it + S - 1) % S) * STAGE * 2, wave);
+      }
     }
     // drain the copies issued past the end before anyone reuses the LDS
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
