@@ -162,7 +162,8 @@ EK_INLINE float fmodf_(float a, float b) { return __builtin_fmodf(a, b); }
 // in register-resident epilogues.
 EK_INLINE float erf_as(float x) {
   const float ax = __builtin_fabsf(x);
-  const float t = 1.0f / __builtin_fmaf(0.3275911f, ax, 1.0f);
+  // v_rcp_f32 (1 ulp) instead of an IEEE division: t's rounding changes erf by < 1e-7
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f, ax, 1.0f));
   float poly = __builtin_fmaf(1.061405429f, t, -1.453152027f);
   poly = __builtin_fmaf(poly, t, 1.421413741f);
   poly = __builtin_fmaf(poly, t, -0.284496736f);
