@@ -193,6 +193,30 @@ def _fast_entry(lc) -> "_FastEntry | None":
 
 
 _tls = threading.local()
+_ek_launch_fn = None
+_raw_stream_fns = None
+
+
+def _ek_launch():
+    global _ek_launch_fn
+    if _ek_launch_fn is None:
+        _ek_launch_fn = _hip.load_library().ek_launch
+    return _ek_launch_fn
+
+
+def _launch_stream() -> int:
+    """torch's current raw stream on the current device (what `device.current_stream`
+    returns) through cached accessors, for the warm path."""
+    global _raw_stream_fns
+    if _raw_stream_fns is None:
+        torch = _torch()
+        c = getattr(torch, "_C", None) if torch is not None else None
+        if c is None or not torch.cuda.is_initialized() or \
+                not hasattr(c, "_cuda_getCurrentRawStream"):
+            return D.current_stream()
+        _raw_stream_fns = (c._cuda_getCurrentRawStream, c._cuda_getDevice)
+    raw, dev = _raw_stream_fns
+    return int(raw(dev()))
 
 
 def _errbuf():
@@ -365,6 +389,7 @@ class JITFunction:
         self._name_set = frozenset(self.arg_names)
         self._cache: dict[Any, Launcher] = {}
         self._fast: dict[Any, _FastEntry] = {}
+        self._binders: dict[tuple, Callable] = {}
 
     def __repr__(self):
         return f"JITFunction({self.fn.__module__}:{self.__name__})"
@@ -539,15 +564,92 @@ class JITFunction:
                 return None
         return tuple(key), rt
 
+    def _make_binder(self, nargs: int, kwnames: tuple, args, kwargs):
+        """A key function for one call shape (the number of positional arguments and the
+        keyword names in order), specialised to the Python types the arguments had when the
+        shape was first seen. It returns what `_fast_key` returns for the same call (the
+        same key tuple, the same runtime values) or None when an argument has another type
+        (then `_fast_key` runs). Generated once per shape, it replaces the per-parameter
+        dispatch of `_fast_key` with straight-line code."""
+        torch = _torch()
+        ns = {"_env": _env_token, "_ic": _int_class, "_sc": _span_class, "_li": _last_index,
+              "_unwrap": core.unwrap, "_pack": struct.pack, "_dtype": core.dtype,
+              "_TT_cls": T.Tensor}
+        lines = [f"def _bind(args, kwargs, nw, dw):"]
+        if nargs:
+            lines.append("    " + ", ".join(f"a{i}" for i in range(nargs)) +
+                         (", = args" if nargs == 1 else " = args"))
+        for k in kwnames:
+            if k not in self._name_set:
+                return lambda *_: None
+            lines.append(f"    k_{k} = kwargs[{k!r}]")
+        parts, rts = [], []
+        for j, prm in enumerate(self.params):
+            if prm.index < nargs:
+                v, sample = f"a{prm.index}", args[prm.index]
+            elif prm.name in kwnames:
+                v, sample = f"k_{prm.name}", kwargs[prm.name]
+            elif prm.default is not inspect.Parameter.empty:
+                v, sample = f"_D{j}", prm.default
+                ns[v] = prm.default
+            else:
+                return lambda *_: None
+            if prm.is_constexpr:
+                lines += [f"    c{j} = _unwrap({v})", f"    t{j} = type(c{j})",
+                          f"    if t{j} is float:", f"        q{j} = (t{j}, _pack('<d', c{j}))",
+                          f"    elif t{j} in (int, bool, str) or isinstance(c{j}, _dtype):",
+                          f"        q{j} = (t{j}, c{j})", "    else:", "        return None"]
+                parts.append(f"q{j}")
+                continue
+            ts = type(sample)
+            if ts is int:
+                lines += [f"    if type({v}) is not int:", "        return None"]
+                parts.append(f"(int, {v} & 15 == 0, {v} == 1, _ic({v}))")
+                rts.append(v)
+            elif ts is float:
+                lines += [f"    if type({v}) is not float:", "        return None"]
+                parts.append(f"(float, {v} > 0)")
+                rts.append(v)
+            elif ts is bool:
+                lines += [f"    if type({v}) is not bool:", "        return None"]
+                parts.append("(bool,)")
+                rts.append(f"int({v})")
+            elif torch is not None and isinstance(sample, torch.Tensor):
+                ns[f"_TT{j}"] = ts
+                lines += [f"    if type({v}) is not _TT{j} or not {v}.is_cuda:", "        return None",
+                          f"    p{j} = {v}.data_ptr()",
+                          f"    l{j} = {v}.numel() - 1 if {v}.is_contiguous() else _li({v})",
+                          f"    s{j} = _sc((l{j} + 1) * {v}.element_size(), l{j})"]
+                parts.append(f"({v}.dtype, p{j} & 15 == 0, s{j})")
+                rts.append(f"p{j}")
+            elif ts is T.Tensor:
+                lines += [f"    if type({v}) is not _TT_cls:", "        return None",
+                          f"    p{j} = {v}.ptr", f"    l{j} = _li({v})"]
+                parts.append(f"({v}.dtype.name, p{j} & 15 == 0, "
+                             f"_sc((l{j} + 1) * {v}.itemsize, l{j}))")
+                rts.append(f"p{j}")
+            else:
+                return lambda *_: None
+        lines.append(f"    return (nw, dw, _env(), {', '.join(parts)}{',' if parts else ''}), "
+                     f"[{', '.join(rts)}]")
+        exec(compile("\n".join(lines), f"<binder {self.__name__}>", "exec"), ns)
+        return ns["_bind"]
+
     def _fast_launch(self, ent: _FastEntry, rt, args, kwargs, grid, stream):
         if callable(grid):
             grid = grid(dict(self._bind(args, kwargs)))
-        grid = tuple(int(g) for g in (grid if isinstance(grid, (tuple, list)) else (grid,)))
-        if not 1 <= len(grid) <= 3:
-            raise ValueError(f"grid must have 1 to 3 dimensions, got {grid}")
-        if grid[0] >= 1 << 31 or any(g > 65535 for g in grid[1:]) or any(g < 0 for g in grid):
-            raise ValueError(f"grid {grid} exceeds the HIP limits (x < 2^31, y, z <= 65535)")
-        gx, gy, gz = (grid + (1, 1))[:3]
+        if type(grid) is tuple and len(grid) == 1 and type(grid[0]) is int and \
+                0 <= grid[0] < 1 << 31:
+            gx, gy, gz = grid[0], 1, 1      # the common 1-D grid, already valid
+        else:
+            grid = tuple(int(g) for g in (grid if isinstance(grid, (tuple, list))
+                                          else (grid,)))
+            if not 1 <= len(grid) <= 3:
+                raise ValueError(f"grid must have 1 to 3 dimensions, got {grid}")
+            if grid[0] >= 1 << 31 or any(g > 65535 for g in grid[1:]) or \
+                    any(g < 0 for g in grid):
+                raise ValueError(f"grid {grid} exceeds the HIP limits (x < 2^31, y, z <= 65535)")
+            gx, gy, gz = (grid + (1, 1))[:3]
         if gx == 0 or gy == 0 or gz == 0:
             return ent.lc.ck
         if _trace._active is not None:
@@ -557,22 +659,29 @@ class JITFunction:
         except (struct.error, OverflowError):
             return None                 # a float beyond fp32's range: general packing
         if stream is None:
-            stream = D.current_stream()
+            stream = _launch_stream()
         t = _timing.current()
         if t is not None:
             t.launch(stream, ent.fn, (gx, gy, gz), ent.block, kb, len(kb))
             return ent.lc.ck
-        lib = _hip.load_library()
         err = _errbuf()
-        if lib.ek_launch(stream or None, ent.fn, gx, gy, gz, ent.block, 1, 1, 0, kb, len(kb),
-                         err, 1024):
+        if _ek_launch()(stream or None, ent.fn, gx, gy, gz, ent.block, 1, 1, 0, kb, len(kb),
+                        err, 1024):
             from enceladus_amd.compiler.errors import HipError
             raise HipError(f"ek_launch: {err.value.decode(errors='replace')}")
         return ent.lc.ck
 
     def run(self, *args, grid, num_warps: int = 4, num_stages=None, dot_warps=None,
             dot_backend: str = "auto", stream=None, **kwargs):
-        fk = self._fast_key(args, kwargs, num_warps, dot_warps) if not self.interpret else None
+        fk = None
+        if not self.interpret:
+            shape = (len(args), tuple(kwargs))
+            b = self._binders.get(shape)
+            if b is None:
+                b = self._binders[shape] = self._make_binder(shape[0], shape[1], args, kwargs)
+            fk = b(args, kwargs, num_warps, dot_warps)
+            if fk is None:
+                fk = self._fast_key(args, kwargs, num_warps, dot_warps)
         if fk is not None:
             ent = self._fast.get(fk[0])
             if ent is not None and (not ent.lc.deps or ent.lc.current()):

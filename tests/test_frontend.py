@@ -344,3 +344,31 @@ def test_bad_arguments_name_the_kernel_and_argument(args, kwargs, phrases):
     assert msg.startswith("_fill: ")
     for p in phrases:
         assert p in msg
+
+
+def test_generated_binder_matches_the_generic_key():
+    """The per-call-shape binder of the warm launch path computes exactly the key and
+    runtime values of the generic key function, and declines (None) when an argument's type
+    differs from the shape's first call (reference: runtime/jit.py:422-461). Scalar
+    arguments only: the device-pointer case is checked on the GPU."""
+    import enceladus
+    import enceladus.language as tl
+
+    @enceladus.jit
+    def s(n, a, flag, BLOCK: tl.constexpr, S: tl.constexpr, NAME: tl.constexpr = "x"):
+        pass
+
+    cases = [((16, 2.0, True), {"BLOCK": 64, "S": 0.5}),
+             ((17, -2.0, False), {"BLOCK": 64, "S": -0.0, "NAME": "y"}),
+             ((1, 0.0, True), {"S": 1.5, "BLOCK": 128}),
+             ((1 << 40, 3.0, False), {"BLOCK": 64, "S": 0.5})]
+    for args, kw in cases:
+        b = s._make_binder(len(args), tuple(kw), args, kw)
+        for nw, dw in ((4, None), (8, (8, 1))):
+            assert b(args, kw, nw, dw) == s._fast_key(args, kw, nw, dw)
+        # another type in the same call shape: the binder declines, the generic key answers
+        other = (float(args[0]),) + args[1:]
+        assert b(other, kw, 4, None) is None
+        assert s._fast_key(other, kw, 4, None) is not None
+    # an unknown keyword: no binder key
+    assert s._make_binder(0, ("nope",), (), {"nope": 1})((), {"nope": 1}, 4, None) is None

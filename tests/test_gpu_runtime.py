@@ -273,6 +273,23 @@ def test_warm_path_respecializes_on_argument_classes():
     assert len(keys) >= 5
 
 
+@pytest.mark.gpu
+def test_binder_keys_match_the_generic_key_on_device_tensors():
+    """With torch device tensors (contiguous, strided views, offset views, other dtypes) the
+    generated binder gives the generic key function's key and pointers."""
+    import torch
+    from examples.vector_add import add_kernel
+    print("[case] binder keys on device tensors", flush=True)
+    base = torch.randn(4096, device="cuda")
+    views = [base, base[1:1001], base[::2], base.view(64, 64)[:, :32],
+             torch.zeros(100, dtype=torch.float16, device="cuda")]
+    for x in views:
+        args = (x, x, x, int(x.numel()))
+        kw = {"BLOCK": 1024}
+        b = add_kernel._make_binder(4, ("BLOCK",), args, kw)
+        assert b(args, kw, 4, None) == add_kernel._fast_key(args, kw, 4, None)
+
+
 WARM_SCALE = 2.0
 
 
