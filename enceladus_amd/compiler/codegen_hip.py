@@ -2270,8 +2270,10 @@ class Emitter:
         tm, tn, tk, kpl = plan.tm, plan.tn, plan.tk, ins.kpl
         dd = getattr(self, "deferred_dma", None)
         copies = {}
-        if (sa or sb) and dd is not None and not dd["used"] and tk > 1:
-            # The loop's stage copies go out from this dot, spread over its k steps: copy c
+        if (sa or sb) and dd is not None and not dd["used"] and tk > 1 and \
+                dd["scope"] is self.cur:
+            # The loop's stage copies go out from this dot (one the loop body always runs,
+            # not one under a branch), spread over its k steps: copy c
             # after the MFMAs of step c * (tk - 1) // n, so each step's copy issue overlaps
             # the MFMAs already queued instead of stalling the wave in one block (the first
             # fragment reads still go out before any copy).
@@ -3019,7 +3021,8 @@ class Emitter:
             self.cur.items.append(slot)
             prev_dma = getattr(self, "deferred_dma", None)
             self.deferred_dma = None if self.opt.get("no_late_dma") else \
-                {"lines": lines, "setup": setup, "chunks": chunks, "used": False}
+                {"lines": lines, "setup": setup, "chunks": chunks, "used": False,
+                 "scope": self.cur}
             if self.deferred_dma is None:
                 slot.extend(self.cur.indent + ln for ln in lines)
         elif stg:

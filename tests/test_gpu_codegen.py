@@ -288,3 +288,37 @@ def test_math_mode_divisions_stay_within_their_bound(mode):
         np.testing.assert_array_equal(s, q_s)
     else:
         assert np.all(np.abs(s - q_s) <= 1.5 * np.spacing(np.abs(q_s)))
+
+
+def test_staged_loop_with_a_dot_under_a_branch():
+    """A loop whose K tiles are staged through LDS by DMA but whose dot runs only on some
+    iterations: the copies of the next stage must still go out on every iteration (they
+    are issued from a dot only when the loop body always runs that dot)."""
+    print("[case] staged loop, dot under a branch", flush=True)
+    import torch
+
+    @enceladus.jit
+    def k(q_ptr, k_ptr, o_ptr, N, BM: tl.constexpr, BN: tl.constexpr, D: tl.constexpr):
+        q_desc = tl.make_tensor_descriptor(q_ptr, [BM, D], [D, 1], [BM, D])
+        k_desc = tl.make_tensor_descriptor(k_ptr, [N, D], [D, 1], [BN, D])
+        q = q_desc.load([0, 0])
+        acc = tl.zeros([BM, BN], tl.float32)
+        for n0 in range(0, N, BN):
+            kt = k_desc.load([n0, 0])
+            if (n0 // BN) % 3 == 0:
+                acc = tl.dot(q, tl.trans(kt), acc)
+        rm = tl.arange(0, BM)[:, None]
+        rn = tl.arange(0, BN)[None, :]
+        tl.store(o_ptr + rm * BN + rn, acc)
+
+    BM, BN, D, N = 64, 64, 64, 512
+    rng = np.random.default_rng(5)
+    q = rng.integers(-3, 4, (BM, D)).astype(np.float16)
+    kk = rng.integers(-3, 4, (N, D)).astype(np.float16)
+    o = torch.zeros((BM, BN), dtype=torch.float32, device="cuda")
+    k[(1,)](torch.from_numpy(q).cuda(), torch.from_numpy(kk).cuda(), o, N, BM=BM, BN=BN, D=D)
+    want = np.zeros((BM, BN), np.float64)
+    for n0 in range(0, N, BN):
+        if (n0 // BN) % 3 == 0:
+            want += q.astype(np.float64) @ kk[n0:n0 + BN].astype(np.float64).T
+    np.testing.assert_array_equal(o.cpu().numpy(), want)
