@@ -2587,7 +2587,8 @@ class Emitter:
         # A tile starting at row >= 0 (the usual case) copies through a resource based at its
         # first row, so the per-chunk offsets are the loop-invariant ones; otherwise rows
         # before 0 need the general form with the row offset in each lane's address. The
-        # choice is uniform, made with selects so the copies need no branch.
+        # choice is uniform: the resource is a select, the rare general offsets a branch in
+        # the set-up, so the copies themselves need no branch.
         setup = [f"const int {t}_r0 = {o0};",
                  f"const uint32_t {t}_ls = ek_dml{idx} + (uint32_t)({stage}) * "
                  f"{info['stage_elems'] * 2}u;",
@@ -2596,11 +2597,15 @@ class Emitter:
                  f"{s0}, {t}_r0 < {sh0} ? (uint32_t)({sh0} - {t}_r0) * (uint32_t){s0} * 2u : 0u) "
                  f": ek::rsrc_words({base}, {t}_r0 > -{R} ? (uint32_t){sh0} * (uint32_t){s0} * 2u "
                  ": 0u);",
-                 f"const int {t}_rb = {t}_r0 * {s0};",
                  f"int {t}_of[{per}];",
                  "#pragma unroll",
-                 f"for (int i = 0; i < {per}; ++i) {t}_of[i] = {t}_pos ? ek_dmb{idx}[i] : "
-                 f"(ek_dmo{idx}[i] >= 0 ? ({t}_rb + ek_dmo{idx}[i]) * 2 : ek::kOOB);"]
+                 f"for (int i = 0; i < {per}; ++i) {t}_of[i] = ek_dmb{idx}[i];",
+                 f"if (!{t}_pos) {{",
+                 f"  const int {t}_rb = {t}_r0 * {s0};",
+                 "  #pragma unroll",
+                 f"  for (int i = 0; i < {per}; ++i) {t}_of[i] = ek_dmo{idx}[i] >= 0 ? "
+                 f"({t}_rb + ek_dmo{idx}[i]) * 2 : ek::kOOB;",
+                 "}"]
         chunks = [f"ek::dma16({t}_rs, {t}_ls + {i * self.nt * 16}u, {t}_of[{i}]);"
                   for i in range(per)]
         return setup, chunks
