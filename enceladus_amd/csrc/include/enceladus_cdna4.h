@@ -240,17 +240,52 @@ template <typename T> EK_INLINE T shfl(T v, int src) {
   }
 }
 
-// Exchange with lane ^ mask. Masks 1 and 2 use DPP quad permutes, which need no LDS
-// hardware; other masks use ds_bpermute.
-template <int MASK, typename T> EK_INLINE T shfl_xor(T v) {
-  if constexpr (sizeof(T) == 4 && (MASK == 1 || MASK == 2)) {
-    int u = __builtin_bit_cast(int, v);
-    // quad_perm selectors: [1,0,3,2] = 0xB1 for xor 1; [2,3,0,1] = 0x4E for xor 2.
-    constexpr int ctrl = MASK == 1 ? 0xB1 : 0x4E;
-    int r = __builtin_amdgcn_mov_dpp(u, ctrl, 0xF, 0xF, false);
-    return __builtin_bit_cast(T, r);
+// A 32-bit exchange with lane ^ MASK that stays in the VALU for every power of two
+// (ds_bpermute, the general path, is an LDS round trip that the reductions would wait on):
+// - 1, 2: one DPP quad permute ([1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E);
+// - 4: row_half_mirror (lane ^ 7), then quad_perm [3,2,1,0] = 0x1B (lane ^ 3);
+// - 8: row_mirror (lane ^ 15), then row_half_mirror (lane ^ 7);
+// - 16: v_permlane16_swap of the value with itself leaves rows (0,0,2,2) in the first
+//   result and rows (1,1,3,3) in the second; a lane takes the other row of its pair;
+// - 32: v_permlane32_swap likewise leaves halves (lo,lo) and (hi,hi).
+template <int MASK> EK_INLINE uint32_t xor_lanes_u32(uint32_t u) {
+  const int x = (int)u;
+  if constexpr (MASK == 1 || MASK == 2) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp(x, MASK == 1 ? 0xB1 : 0x4E, 0xF, 0xF, false);
+  } else if constexpr (MASK == 4) {
+    const int t = __builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, false);
+    return (uint32_t)__builtin_amdgcn_mov_dpp(t, 0x1B, 0xF, 0xF, false);
+  } else if constexpr (MASK == 8) {
+    const int t = __builtin_amdgcn_mov_dpp(x, 0x140, 0xF, 0xF, false);
+    return (uint32_t)__builtin_amdgcn_mov_dpp(t, 0x141, 0xF, 0xF, false);
+  } else if constexpr (MASK == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return (lane_id() & 16) ? (uint32_t)r[0] : (uint32_t)r[1];
+  } else if constexpr (MASK == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return (lane_id() & 32) ? (uint32_t)r[0] : (uint32_t)r[1];
   } else {
-    return shfl(v, lane_id() ^ MASK);
+    return shfl_u32(u, lane_id() ^ MASK);
+  }
+}
+
+// Exchange with lane ^ MASK, for values of up to 8 bytes (all lanes active).
+template <int MASK, typename T> EK_INLINE T shfl_xor(T v) {
+  if constexpr (sizeof(T) == 8) {
+    uint64_t u;
+    __builtin_memcpy(&u, &v, 8);
+    const uint32_t lo = xor_lanes_u32<MASK>((uint32_t)u), hi = xor_lanes_u32<MASK>((uint32_t)(u >> 32));
+    u = ((uint64_t)hi << 32) | lo;
+    T r;
+    __builtin_memcpy(&r, &u, 8);
+    return r;
+  } else {
+    uint32_t u = 0;
+    __builtin_memcpy(&u, &v, sizeof(T));
+    u = xor_lanes_u32<MASK>(u);
+    T r;
+    __builtin_memcpy(&r, &u, sizeof(T));
+    return r;
   }
 }
 

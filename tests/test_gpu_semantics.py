@@ -385,3 +385,41 @@ def test_scan_of_an_interleaved_view(reverse):
         wa, wb = _affine_ref(a.T.reshape(-1), b.T.reshape(-1), 0, reverse)
     np.testing.assert_array_equal(oa, wa)
     np.testing.assert_array_equal(ob, wb)
+
+
+_XOR_LANES = '''
+#include "enceladus_cdna4.h"
+template <int M> __device__ void one(uint32_t* o32, unsigned long long* o64, uint16_t* o16, int slot) {
+  const int t = threadIdx.x, n = blockDim.x;
+  const uint32_t v = 0x9E3779B9u * (uint32_t)(t + 1);
+  o32[slot * n + t] = ek::shfl_xor<M>(v);
+  o64[slot * n + t] = ek::shfl_xor<M>(((unsigned long long)v << 32) | (uint32_t)~t);
+  o16[slot * n + t] = ek::shfl_xor<M>((uint16_t)(v >> 7));
+}
+extern "C" __global__ void xor_lanes(uint32_t* o32, unsigned long long* o64, uint16_t* o16) {
+  one<1>(o32, o64, o16, 0); one<2>(o32, o64, o16, 1); one<4>(o32, o64, o16, 2);
+  one<8>(o32, o64, o16, 3); one<16>(o32, o64, o16, 4); one<32>(o32, o64, o16, 5);
+}
+'''
+
+
+def test_lane_exchanges_match_lane_xor():
+    """`ek::shfl_xor<m>`, the lane butterfly of every reduction, returns lane ^ m's value
+    for m = 1..32 and 16-, 32- and 64-bit values (DPP permutes, row mirrors and the gfx950
+    permlane swaps), in every wave of a 4-wave workgroup."""
+    _say("lane exchanges")
+    k = enceladus.hip_kernel(_XOR_LANES, "xor_lanes")
+    n = 256
+    o32 = np.zeros((6, n), np.uint32)
+    o64 = np.zeros((6, n), np.uint64)
+    o16 = np.zeros((6, n), np.uint16)
+    k[1, n](o32, o64, o16)
+    t = np.arange(n, dtype=np.uint64)
+    v = (np.uint64(0x9E3779B9) * (t + np.uint64(1))) & np.uint64(0xFFFFFFFF)
+    v64 = (v << np.uint64(32)) | (~t & np.uint64(0xFFFFFFFF))
+    for i in range(6):
+        src = (np.arange(n) ^ (1 << i))
+        np.testing.assert_array_equal(o32[i], v[src].astype(np.uint32), err_msg=f"xor {1 << i}")
+        np.testing.assert_array_equal(o64[i], v64[src], err_msg=f"xor {1 << i}")
+        np.testing.assert_array_equal(o16[i], ((v[src] >> np.uint64(7)) & np.uint64(0xFFFF)).astype(np.uint16),
+                                      err_msg=f"xor {1 << i}")
