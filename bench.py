@@ -13,7 +13,8 @@ the CPU oracle. Matmul and attention take the variant the library's autotuner pi
 (`matmul_desc_tuned`, `matmul_bias_gelu_tuned`, `attention_tuned_kernel` over
 `enceladus.configs`); the HBM-bound rows time each listed `num_warps` and report the
 fastest. Kernel times come from HIP events recorded on the launch stream (torch's current
-stream) around K pre-packed launches after W warm-ups; inputs of the HBM-bound rows rotate
+stream) around K pre-packed launches after W warm-ups and at least 50 ms of GPU time spent
+warming up (as the reference's do_bench); inputs of the HBM-bound rows rotate
 over buffer sets totalling > 600 MB so the 256 MB Infinity Cache cannot serve them.
 
 The CPU baseline (`cpu_baseline`, and `cpu` under each workload) times the oracle
@@ -48,6 +49,7 @@ os.environ.setdefault("ENCELADUS_CACHE_DIR", os.path.join(ROOT, ".ek_cache"))
 
 HBM_PEAK = 8.0e12          # bytes/s (MI355X HBM3E)
 MFMA_PEAK_F16 = 2.5e15     # dense fp16/bf16 FLOP/s
+WARMUP_MS = 50.0           # GPU time spent warming up before each timed region
 METRIC = "matmul/flash-attn TFLOP/s, softmax GB/s, % of MI355X roofline"
 
 
@@ -61,12 +63,26 @@ class Timer:
     def __init__(self, torch):
         self.torch = torch
 
-    def run(self, launches, steps, warmup):
+    def run(self, launches, steps, warmup, warmup_ms=WARMUP_MS):
+        """ms per launch over `steps` launches, after `warmup` launches and then more
+        until the GPU has been busy for `warmup_ms` (the reference's do_bench warms up by
+        GPU time the same way, testing.py:14-63: the clock is low after idle, and a
+        kernel's first launches after an idle spell run up to 20% slower)."""
         torch = self.torch
         for i in range(warmup):
             launches[i % len(launches)]()
         torch.cuda.synchronize()
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        spent, batch, i = 0.0, 1, warmup
+        while spent < warmup_ms:
+            s.record()
+            for _ in range(batch):
+                launches[i % len(launches)]()
+                i += 1
+            e.record()
+            torch.cuda.synchronize()
+            spent += s.elapsed_time(e)
+            batch = min(2 * batch, 64)
         s.record()
         for i in range(steps):
             launches[i % len(launches)]()

@@ -3287,24 +3287,32 @@ class Emitter:
             # programs' global loads before the first program's LDS atomics: a workgroup
             # keeps U loads in flight instead of one.
             u_ = max(1, int(self.opt.get("coarsen_unroll", 4)))
-            pids = ["  const int ek_pid_x = ek_p % ek_np_x;",
-                    "  const int ek_pid_y = (ek_p / ek_np_x) % ek_np_y;",
-                    "  const int ek_pid_z = ek_p / (ek_np_x * ek_np_y);",
+            # The walk is emitted twice: a 1-D launch (the common case) takes the program id
+            # as is, other launches split it with integer divisions per program.
+            flat = ["  const int ek_pid_x = ek_p, ek_pid_y = 0, ek_pid_z = 0;",
                     "  (void)ek_pid_x; (void)ek_pid_y; (void)ek_pid_z;"]
+            general = ["  const int ek_pid_x = ek_p % ek_np_x;",
+                       "  const int ek_pid_y = (ek_p / ek_np_x) % ek_np_y;",
+                       "  const int ek_pid_z = ek_p / (ek_np_x * ek_np_y);",
+                       "  (void)ek_pid_x; (void)ek_pid_y; (void)ek_pid_z;"]
             out.append("  const int ek_nprog = ek_np_x * ek_np_y * ek_np_z;")
             out.append("  const int ek_g = (int)gridDim.x;")
-            out.append("  int ek_p0 = blockIdx.x;")
-            if u_ > 1:
-                out.append(f"  for (; ek_p0 + {u_ - 1} * ek_g < ek_nprog; ek_p0 += {u_} * ek_g) {{")
-                for k_ in range(u_):
-                    out.append(f"  {{ const int ek_p = ek_p0 + {k_} * ek_g;")
-                    out.extend(pids)
-                    out.extend(body)
+            for n_, pids in enumerate((flat, general)):
+                out.append("  if (ek_np_y == 1 && ek_np_z == 1) {" if n_ == 0 else "  } else {")
+                out.append("  int ek_p0 = blockIdx.x;")
+                if u_ > 1:
+                    out.append(f"  for (; ek_p0 + {u_ - 1} * ek_g < ek_nprog; "
+                               f"ek_p0 += {u_} * ek_g) {{")
+                    for k_ in range(u_):
+                        out.append(f"  {{ const int ek_p = ek_p0 + {k_} * ek_g;")
+                        out.extend(pids)
+                        out.extend(body)
+                        out.append("  }")
                     out.append("  }")
+                out.append("  for (int ek_p = ek_p0; ek_p < ek_nprog; ek_p += ek_g) {")
+                out.extend(pids)
+                out.extend(body)
                 out.append("  }")
-            out.append("  for (int ek_p = ek_p0; ek_p < ek_nprog; ek_p += ek_g) {")
-            out.extend(pids)
-            out.extend(body)
             out.append("  }")
         else:
             out.extend(body)
