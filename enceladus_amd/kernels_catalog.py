@@ -67,8 +67,10 @@ def _input_shapes(wl) -> dict:
         return {"x": ((W.VADD_N,), "float32"), "y": ((W.VADD_N,), "float32")}
     if wl.name in ("softmax", "copy_rows"):
         return {"x": ((W.ROWS, W.COLS), "float32")}
-    if wl.name == "copy_flat":
+    if wl.name in ("copy_flat", "read_flat"):
         return {"x": ((W.ROWS * W.COLS,), "float32")}
+    if wl.name == "fill_flat":
+        return {}
     if wl.name == "rmsnorm":
         return {"x": ((W.ROWS, W.COLS), "float32"), "w": ((W.COLS,), "float32")}
     if wl.name.startswith("matmul"):

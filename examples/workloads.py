@@ -245,6 +245,31 @@ def copy_flat_kernel(out_ptr, in_ptr, n, BLOCK: tl.constexpr):
     tl.store(out_ptr + offs, tl.load(in_ptr + offs, mask=mask), mask=mask)
 
 
+@enceladus.jit
+def read_flat_kernel(out_ptr, in_ptr, n, BLOCK: tl.constexpr):
+    offs = tl.program_id(0) * BLOCK + tl.arange(0, BLOCK)
+    x = tl.load(in_ptr + offs, mask=offs < n, other=0.0)
+    tl.store(out_ptr + tl.program_id(0), tl.max(x, axis=0))
+
+
+@enceladus.jit
+def fill_flat_kernel(out_ptr, value, n, BLOCK: tl.constexpr):
+    offs = tl.program_id(0) * BLOCK + tl.arange(0, BLOCK)
+    tl.store(out_ptr + offs, tl.full([BLOCK], value, tl.float32), mask=offs < n)
+
+
+def _read_flat_args(b, v):
+    n = b["x"].numel()
+    block = dict(v.constexprs)["BLOCK"]
+    return ((n + block - 1) // block,), (b["out"], b["x"], n)
+
+
+def _fill_flat_args(b, v):
+    n = b["out"].numel()
+    block = dict(v.constexprs)["BLOCK"]
+    return ((n + block - 1) // block,), (b["out"], 1.5, n)
+
+
 def _copy_rows_args(b, v):
     m, n = b["x"].shape
     return (m,), (b["out"], b["x"], n, n)
@@ -316,6 +341,20 @@ def table() -> dict[str, Workload]:
         ROWS * COLS * 8, "fp32", lambda: {"x": _f32(0, ROWS * COLS)},
         {"out": ((ROWS * COLS,), "float32")}, _copy_flat_args,
         [Variant((("BLOCK", b),), 4) for b in (1024, 2048, 4096)], ceiling=True)
+    # One direction only, over the same 2^25 fp32 elements: the read and write rates
+    # whose mix bounds every row above (a max per tile, whose 4-byte results are not
+    # counted; a constant fill).
+    w["read_flat"] = Workload(
+        "read_flat", "fp32 2^25 elements read, max per tile", lambda: read_flat_kernel,
+        "hbm", ROWS * COLS * 4, "fp32",
+        lambda: {"x": _f32(0, ROWS * COLS)}, {"out": ((ROWS * COLS // 1024,), "float32")},
+        _read_flat_args, [Variant((("BLOCK", b),), 4) for b in (1024, 2048, 4096)],
+        ceiling=True)
+    w["fill_flat"] = Workload(
+        "fill_flat", "fp32 2^25 elements written", lambda: fill_flat_kernel, "hbm",
+        ROWS * COLS * 4, "fp32", lambda: {}, {"out": ((ROWS * COLS,), "float32")},
+        _fill_flat_args, [Variant((("BLOCK", b),), 4) for b in (1024, 2048, 4096)],
+        ceiling=True)
     return w
 
 

@@ -17,7 +17,8 @@ against the CPU oracle (reference protocol: tests/conftest.py:102-145):
 - flash attention bf16 [4,32,4096,128] causal and [4,32,1024,128]: the oracle on a sample of
   (start_m, batch*head) programs stratified over start_m (first, middle, last blocks) and
   the float64 closed form on the same rows;
-- the two copy kernels the benchmark reports as HBM ceilings: bit-exact.
+- the two copy kernels the benchmark reports as HBM ceilings: bit-exact; the read-only
+  (max per tile) and write-only (fill) ceilings: exact.
 
 Tolerances: the reference's by output dtype (tests/conftest.py:75-79): fp32 (1e-5, 1e-5)
 with atol 1e-8 for softmax outputs of ~1/8192; fp16 (atol 1e-3, rtol 2e-3); bf16
@@ -157,6 +158,27 @@ def test_copy_ceilings_full(name, v):
     _say(f"{name} {v.label}")
     b, _ = _run(name, v)
     assert np.array_equal(b["out"].cpu().numpy(), _host(name)["x"])
+
+
+@pytest.mark.parametrize("v", _params("read_flat"))
+def test_read_ceiling_full(v):
+    """The read-only ceiling kernel: each program's max matches the closed form exactly
+    (a max is exact in any order)."""
+    _say(f"read_flat {v.label}")
+    b, _ = _run("read_flat", v)
+    x = _host("read_flat")["x"]
+    block = dict(v.constexprs)["BLOCK"]
+    want = x.reshape(-1, block).max(axis=1)
+    got = b["out"].cpu().numpy()[:want.size]
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("v", _params("fill_flat"))
+def test_fill_ceiling_full(v):
+    """The write-only ceiling kernel stores the constant into every element."""
+    _say(f"fill_flat {v.label}")
+    b, _ = _run("fill_flat", v)
+    assert np.all(b["out"].cpu().numpy() == np.float32(1.5))
 
 
 HIST_SIZES = [W.HIST_N, W.HIST_N + 3 * 1024 + 5]
