@@ -294,7 +294,7 @@ def table() -> dict[str, Workload]:
     w["vector_add"] = Workload(
         "vector_add", "fp32 n=2^28 BLOCK 1024", _k("vector_add", "add_kernel"), "hbm",
         12 * VADD_N, "fp32", _vadd_inputs, {"out": ((VADD_N,), "float32")}, _vadd_args,
-        [Variant((("BLOCK", 1024),), 4)])
+        [Variant((("BLOCK", 1024),), nw) for nw in (4, 2)])
     w["softmax"] = Workload(
         "softmax", "fp32 [4096, 8192]", _k("softmax", "softmax_kernel"), "hbm",
         ROWS * COLS * 8, "fp32", _row_inputs, {"out": ((ROWS, COLS), "float32")},
