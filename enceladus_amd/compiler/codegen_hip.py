@@ -455,7 +455,8 @@ class Emitter:
             self.kind[res.id] = "anchored"
             lay = self.mem_layout(op.operands[0])
             us = self.uses.get(res.id, [])
-            if len(us) == 1 and us[0].name == "scan":
+            if len(us) == 1 and us[0].name == "scan" and \
+                    LY.scan_groups(lay, us[0].attrs["axis"]) is None:
                 lay = LY.scan_layout(res.type.shape, us[0].attrs["axis"], self.nw)
             self.lay[res.id] = lay
         elif n == "desc_load" and res.id in self.staged:
@@ -489,7 +490,7 @@ class Emitter:
             src = op.operands[0]
             ax = op.attrs["axis"]
             sl = self.lay[src.id] if self._anch(src) else None
-            if sl is None or not LY.scan_friendly(sl, ax):
+            if sl is None or LY.scan_groups(sl, ax) is None:
                 sl = LY.scan_layout(src.type.shape, ax, self.nw)
             self.kind[res.id] = "anchored"
             self.lay[res.id] = sl
@@ -2017,9 +2018,20 @@ class Emitter:
         arr = self.array(src, lay)
         nm = self.fresh("sc")
         R = lay.nregs
-        k = sum(1 for b in lay.reg if b[0] == ax)
+        k, gpos = LY.scan_groups(lay, ax)
         run = 1 << k
         outer = R // run
+        # the axis segment (group) each run of registers belongs to, and the same run's
+        # register-run index in another group
+        gbits = [g - k for g in gpos]
+        gmask = sum(1 << b for b in gbits)
+        G = 1 << len(gbits)
+
+        def grp(o):
+            return sum(((o >> b) & 1) << j for j, b in enumerate(gbits))
+
+        def in_grp(o, g):
+            return (o & ~gmask) | sum(((g >> j) & 1) << b for j, b in enumerate(gbits))
         cin = (lambda x: f"ek::f32({x})") if is_half(dt) else (lambda x: x)
         self.emit(f"{acc_t} {nm}_x[{R}];")
         self.emit("#pragma unroll")
@@ -2064,22 +2076,29 @@ class Emitter:
                 self.emit(f"for (int o = 0; o < {outer}; ++o) {{ {acc_t} u = ek::shfl({nm}_p[o], "
                           f"{srcl}); if ({cond}) {nm}_p[o] += u; }}")
                 low |= bit
+            lane_ax = sum(1 << i for i in lane_bits)
+            if G > 1:
+                # each segment's total over the lanes and warps that hold the axis
+                self.emit(f"{acc_t} {nm}_g[{outer}];")
             # warp totals through LDS
             if warp_bits:
                 nwa = 1 << len(warp_bits)
                 rows = res.type.numel // res.type.shape[ax]
                 esz = 8 if acc_t in ("int64_t", "uint64_t") else 4
-                self.need_lds(nwa * rows * esz)
+                self.need_lds(nwa * G * rows * esz)
                 widx = bits_expr("ek_warp", [(w, t) for t, w in enumerate(warp_bits)])
-                lane_ax = sum(1 << i for i in lane_bits)
                 rowc = self._row_lin(lay, ax, f"o * {run}")
+                gsel = "0"
+                if G > 1:
+                    gsel = " | ".join(f"(((o >> {b}) & 1) << {j})" for j, b in enumerate(gbits))
+                slot = f"(({{w}}) * {G} + ({gsel})) * {rows} + {rowc}"
                 writer = f"(ek_lane & {lane_ax}) == {lane_ax if not rev else 0}"
                 self.emit("{")
                 self.emit(f"  {acc_t}* sm = reinterpret_cast<{acc_t}*>(ek_smem);")
                 self.emit("  __syncthreads();")
                 self.emit(f"  if ({writer}) {{")
                 self.emit("    #pragma unroll")
-                self.emit(f"    for (int o = 0; o < {outer}; ++o) sm[({widx}) * {rows} + {rowc}]"
+                self.emit(f"    for (int o = 0; o < {outer}; ++o) sm[{slot.format(w=widx)}]"
                           f" = {nm}_p[o];")
                 self.emit("  }")
                 self.emit("  __syncthreads();")
@@ -2088,13 +2107,30 @@ class Emitter:
                 self.emit(f"  for (int o = 0; o < {outer}; ++o) {{")
                 self.emit(f"    {acc_t} s = 0;")
                 if not rev:
-                    self.emit(f"    for (int w = 0; w < ek_wa; ++w) s += sm[w * {rows} + {rowc}];")
+                    self.emit(f"    for (int w = 0; w < ek_wa; ++w) s += sm[{slot.format(w='w')}];")
                 else:
-                    self.emit(f"    for (int w = ek_wa + 1; w < {nwa}; ++w) s += sm[w * {rows} + "
-                              f"{rowc}];")
+                    self.emit(f"    for (int w = ek_wa + 1; w < {nwa}; ++w) s += "
+                              f"sm[{slot.format(w='w')}];")
+                if G > 1:
+                    self.emit(f"    {acc_t} a = 0;")
+                    self.emit(f"    for (int w = 0; w < {nwa}; ++w) a += sm[{slot.format(w='w')}];")
+                    self.emit(f"    {nm}_g[o] = a;")
                 self.emit(f"    {nm}_p[o] += s;")
                 self.emit("  }")
                 self.emit("}")
+            elif G > 1:
+                # one wave holds the axis: its last lane (first, reversed) has the total
+                src_l = f"(ek_lane | {lane_ax})" if not rev else f"(ek_lane & ~{lane_ax})"
+                self.emit("#pragma unroll")
+                self.emit(f"for (int o = 0; o < {outer}; ++o) {nm}_g[o] = "
+                          f"ek::shfl({nm}_p[o], {src_l});")
+            if G > 1:
+                # segment carries: the totals of the segments before this one (after, reversed)
+                for o in range(outer):
+                    g = grp(o)
+                    prev = [in_grp(o, h) for h in (range(g) if not rev else range(g + 1, G))]
+                    terms = " + ".join(f"{nm}_g[{q}]" for q in prev) if prev else "0"
+                    self.emit(f"{nm}_p[{o}] += {terms};")
             self.emit("#pragma unroll")
             self.emit(f"for (int o = 0; o < {outer}; ++o) {{ {acc_t} e = {nm}_p[o] - {nm}_t[o];")
             self.emit("  #pragma unroll")

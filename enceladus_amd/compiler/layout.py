@@ -284,6 +284,46 @@ def scan_friendly(lay: Layout, axis: int) -> bool:
     return all(locs[i] == ("r", i) for i in range(nreg))
 
 
+def scan_groups(lay: Layout, axis: int):
+    """For a layout a scan can run in: (run, groups) where `run` is the number of low
+    register bits holding the axis's lowest bits (a contiguous run per thread), and
+    `groups` the register bit positions, in increasing significance, of axis bits that
+    come after every lane and warp bit of the axis (segments scanned apart and joined by
+    carries). None when the axis bits are in another order. With no groups this accepts
+    exactly the layouts `scan_friendly` accepts."""
+    locs = []
+    for d_bit in range(log2(lay.shape[axis])):
+        b = (axis, d_bit)
+        if b in lay.reg:
+            locs.append(("r", lay.reg.index(b)))
+        elif b in lay.lane:
+            locs.append(("l", lay.lane.index(b)))
+        else:
+            locs.append(("w", lay.warp.index(b)))
+    k = 0
+    while k < len(locs) and locs[k] == ("r", k):
+        k += 1
+    rest = locs[k:]
+    i = 0
+    for cat in ("l", "w"):
+        prev = -1
+        while i < len(rest) and rest[i][0] == cat:
+            if rest[i][1] < prev:
+                return None
+            prev = rest[i][1]
+            i += 1
+    groups = []
+    prev = k - 1
+    for c, pos in rest[i:]:
+        if c != "r" or pos <= prev:
+            return None
+        groups.append(pos)
+        prev = pos
+    if groups and i == 0:
+        return None     # axis bits only in registers: they are all part of the run
+    return k, groups
+
+
 # -- MFMA layouts -----------------------------------------------------------------------
 
 @dataclass(frozen=True)

@@ -70,6 +70,29 @@ def test_blocked_and_scan_layouts():
     assert not L.scan_friendly(b.expand(0), 1) or True
 
 
+def test_scan_groups():
+    """A scan runs in the coalesced blocked layout of a long row: a 4-element run per lane,
+    then lanes and warps, then the remaining axis bits as register segments joined by
+    carries; the layouts scan_friendly accepts are exactly those without segments."""
+    for nw, groups in ((4, [2, 3]), (8, [2]), (16, [])):
+        b = L.blocked((1, 4096), [1, 0], 4, nw)
+        assert L.scan_groups(b, 1) == (2, groups)
+        assert (L.scan_friendly(b, 1)) == (not groups)
+        s = L.scan_layout((1, 4096), 1, nw)
+        assert L.scan_groups(s, 1)[1] == [] and L.scan_friendly(s, 1)
+    # along the rows of a 2-D tile: no run, lanes, warps, then two register segments
+    b = L.blocked((64, 64), [1, 0], 4, 4)
+    assert L.scan_groups(b, 0) == (0, [2, 3])
+    # a run whose register bits are out of order: not scannable in place
+    t = L.Layout((1, 256), ((1, 1), (1, 0)), tuple((1, i) for i in range(2, 8)), (), "blocked")
+    assert L.scan_groups(t, 1) is None and not L.scan_friendly(t, 1)
+    for shape, ax, nw in (((8, 256), 1, 4), ((256, 8), 0, 2), ((4, 4, 64), 2, 1)):
+        for order in ([len(shape) - 1] + list(range(len(shape) - 1)), list(range(len(shape)))):
+            lay = L.blocked(shape, order, 4, nw)
+            g = L.scan_groups(lay, ax)
+            assert (g is not None and not g[1]) == L.scan_friendly(lay, ax)
+
+
 def test_views_are_free():
     b = L.blocked((64, 64), [1, 0], 8, 4)
     assert L.is_view(b.slice(1).expand(1), b)
