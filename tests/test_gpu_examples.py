@@ -101,6 +101,23 @@ def test_cumsum_int32(shape, reverse):
     assert np.array_equal(got, R.cumsum(x, reverse))
 
 
+@pytest.mark.parametrize("num_warps", [1, 2, 8])
+@pytest.mark.parametrize("reverse", [False, True])
+def test_cumsum_segmented_rows(num_warps, reverse):
+    """Rows longer than one pass of the workgroup's 16-byte vectors are scanned in segments
+    joined by carries: 8 segments in one wave (carries through lane shuffles), 4 over two
+    waves and 1 over eight (through LDS), two rows per program, both directions."""
+    from examples.cumsum import cumsum, cumsum_kernel
+    _say(f"cumsum segmented (6, 2000) num_warps={num_warps} reverse={reverse}")
+    x = np.random.default_rng(3).integers(-100, 100, (6, 2000), dtype=np.int32)
+    got = cumsum(x, reverse, num_warps=num_warps)
+    want = np.empty_like(x)
+    O.run_grid(cumsum_kernel, (3,), want, x, 6, 2000, 2000, 2000, REVERSE=reverse,
+               BLOCK_M=2, BLOCK_N=2048)
+    assert np.array_equal(got, want)
+    assert np.array_equal(got, R.cumsum(x, reverse))
+
+
 @pytest.mark.parametrize("n,bins", [(1 << 20, 1024), (100_003, 64), (5000, 4096),
                                     (70_001, 100), (70_001, 6)])
 @pytest.mark.parametrize("flush", ["two_level", "atomic"])

@@ -8,7 +8,8 @@ tests/test_atomics_scans.py:200-227):
 - layernorm in fp32/fp16, block 256 on rows of 256 and 1000;
 - matmul + bias + GELU on the ragged 200 x 96 x 130 in fp32/fp16;
 - fused GELU in fp32/fp16/bf16; RMSNorm in fp32/fp16 with N(0,1) weights;
-- cumsum in fp32/fp16/bf16/int8/int64, forward and reverse, on (5, 1000), (64, 32), (3, 7);
+- cumsum in fp32/fp16/bf16/int8/int64, forward and reverse, on (5, 1000), (64, 32), (3, 7)
+  and (3, 3000) (rows scanned in segments);
 - the histogram example on float N(0,1) input over [-3, 3) in 48 bins, out-of-range values
   masked (bins of negative and fractional values through `floor`).
 
@@ -194,7 +195,7 @@ def test_rmsnorm_dtypes(dtype, shape):
 
 
 @pytest.mark.parametrize("reverse", [False, True])
-@pytest.mark.parametrize("shape", [(5, 1000), (64, 32), (3, 7)])
+@pytest.mark.parametrize("shape", [(5, 1000), (64, 32), (3, 7), (3, 3000)])
 @pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16", "int8", "int64"])
 def test_cumsum_dtypes(dtype, shape, reverse):
     import enceladus
