@@ -369,3 +369,38 @@ def test_math_modes_pick_division_or_reciprocal():
     assert "(1.0f / " in src("fast", False)
     with pytest.raises(ValueError, match="math_mode"):
         enceladus.jit(math_mode="precise")(lambda x: x)
+
+
+@enceladus.jit
+def _masked_add(x_ptr, y_ptr, o_ptr, n, BLOCK: tl.constexpr):
+    offs = tl.program_id(0) * BLOCK + tl.arange(0, BLOCK)
+    m = offs < n
+    tl.store(o_ptr + offs, tl.load(x_ptr + offs, mask=m) + tl.load(y_ptr + offs, mask=m), mask=m)
+
+
+@enceladus.jit
+def _store_then_load(x_ptr, o_ptr, n, BLOCK: tl.constexpr):
+    offs = tl.program_id(0) * BLOCK + tl.arange(0, BLOCK)
+    tl.store(o_ptr + offs, tl.load(x_ptr + offs, mask=offs < n), mask=offs < n)
+    tl.store(o_ptr + n + offs, tl.load(x_ptr + n + offs, mask=offs < 2 * n), mask=offs < 2 * n)
+
+
+def test_program_versioning():
+    """A straight-line masked program gets one guarded copy without mask tests, which
+    returns, ahead of the general copy; the general copy keeps only the masked paths; its
+    streaming loads wait for the previous one. A guard that would follow a store is not
+    taken (the general copy must start before any store), and the switch turns it off."""
+    x = np.zeros(4, np.float32)
+    f = _masked_add.ir_for(x, x, x, 1 << 20, BLOCK=1024)
+    src = codegen_hip.generate(f).source
+    fast, general = src.split("return;")
+    assert fast.count("__builtin_expect(") == 1
+    assert "vload_nt" in fast and " ? *" not in fast and fast.count("vstore_nt") == 1
+    assert fast.count("__builtin_amdgcn_s_waitcnt(0x0F70)") == 1
+    assert "__builtin_expect(" not in general and " ? *" in general
+    off = codegen_hip.generate(f, {"no_program_versioning": True}).source
+    assert "return;" not in off and "__builtin_expect(" not in off
+    serial = codegen_hip.generate(f, {"no_serial_streams": True}).source
+    assert "__builtin_amdgcn_s_waitcnt(0x0F70)" not in serial
+    two = codegen_hip.generate(_store_then_load.ir_for(x, x, 1 << 20, BLOCK=1024)).source
+    assert "__builtin_expect(" not in two
