@@ -147,8 +147,17 @@ template <typename T> EK_INLINE T rnd(float x) { return cvt<T>(x); }
 // ---------------------------------------------------------------------------
 template <typename T> EK_INLINE T idiv(T a, T b) { return b == (T)0 ? a : (T)(a / b); }
 template <typename T> EK_INLINE T imod(T a, T b) { return b == (T)0 ? (T)0 : (T)(a % b); }
+template <int N> struct uint_of;
+template <> struct uint_of<1> { typedef uint8_t type; };
+template <> struct uint_of<2> { typedef uint16_t type; };
+template <> struct uint_of<4> { typedef uint32_t type; };
+template <> struct uint_of<8> { typedef uint64_t type; };
+// The left shift runs on the unsigned type of the same width, so bits shifted into or
+// past the sign bit wrap instead of being undefined behaviour; a negative count (huge as
+// an unsigned number) or one >= the width gives 0, as NumPy's left_shift does.
 template <typename T> EK_INLINE T ishl(T a, T b) {
-  return ((uint64_t)b >= sizeof(T) * 8) ? (T)0 : (T)(a << b);
+  typedef typename uint_of<sizeof(T)>::type U;
+  return ((uint64_t)b >= sizeof(T) * 8) ? (T)0 : (T)(U)((U)a << b);
 }
 template <typename T> EK_INLINE T ishr(T a, T b) {
   if ((uint64_t)b >= sizeof(T) * 8) return (T)((T)-1 > (T)0 ? 0 : (a < (T)0 ? (T)-1 : (T)0));

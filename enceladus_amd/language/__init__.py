@@ -3,6 +3,7 @@
 Names follow the reference surface (reference: src/enceladus/language/__init__.py:21-102).
 """
 
+from enceladus_amd.compiler.errors import CompilationError
 from enceladus_amd.language import math  # noqa: F401
 from enceladus_amd.language.core import (  # noqa: F401
     bfloat16, constexpr, dtype, float16, float32, int1, int8, int16, int32, int64, uint8,
@@ -25,9 +26,15 @@ from enceladus_amd.language.ops import reduce_ as reduce  # noqa: F401
 from enceladus_amd.language.ops import sum_ as sum  # noqa: F401
 
 
+class _MissingNameError(CompilationError, AttributeError):
+    """A missing `tl` name: a `CompilationError` in a kernel that `hasattr` still handles
+    (reference: language/__init__.py:100-115)."""
+
+
 def __getattr__(name: str):
     if name.startswith("__"):
         raise AttributeError(name)
     if name in ("float64", "double", "fp64"):
-        raise AttributeError("Enceladus has no float64 type. Use tl.float32 instead.")
-    raise AttributeError(f"module `enceladus.language` has no attribute `{name}`")
+        raise _MissingNameError("Enceladus has no float64 type. Use tl.float32 instead.")
+    raise _MissingNameError(f"module `enceladus.language` has no attribute `{name}`. Check "
+                            "the spelling; some Triton functions don't exist in Enceladus.")

@@ -10,6 +10,7 @@ atomic_add :1943, cumsum :2064, associative_scan :2097).
 from __future__ import annotations
 
 import builtins as _bi
+import inspect
 import math as _pymath
 from typing import Any
 
@@ -24,6 +25,12 @@ class Builtin:
         self.__name__ = name
         self._ek_frontend = frontend
         self.__doc__ = frontend.__doc__
+
+    @property
+    def __signature__(self) -> inspect.Signature:
+        """The signature user code calls: the frontend's without the compiler context."""
+        sig = inspect.signature(self._ek_frontend)
+        return sig.replace(parameters=list(sig.parameters.values())[1:])
 
     def __call__(self, *args, **kwargs):
         raise RuntimeError(f"tl.{self.__name__} can only be called inside an @enceladus.jit "
@@ -337,8 +344,8 @@ F.TILE_METHODS["to"] = _to
 
 
 @builtin()
-def cast(ctx, input, dtype, bitcast=False, fp_downcast_rounding=None):
-    return _to(ctx, input, dtype, bitcast)
+def cast(ctx, x, dtype, bitcast=False, fp_downcast_rounding=None):
+    return _to(ctx, x, dtype, bitcast)
 
 
 for _m in ("exp", "exp2", "log", "log2", "sqrt", "rsqrt", "sin", "cos", "tanh", "sigmoid",
@@ -867,14 +874,18 @@ def atomic_cas(ctx, pointer, cmp, val, sem=None, scope=None):
 class _StaticRange:
     _ek_static_range = True
 
-    def __call__(self, *a):
+    def __call__(self, arg1, arg2=None, step=None):
         raise RuntimeError("tl.static_range can only be used in a kernel `for` loop")
 
 
 class _Range:
+    """`tl.range`: the Triton hints `num_stages`, `loop_unroll_factor`,
+    `disallow_acc_multi_buffer`, `flatten` and `warp_specialize` are accepted and have no
+    effect (reference: language/ops.py:1299-1311)."""
     _ek_range = True
 
-    def __call__(self, *a, **k):
+    def __call__(self, arg1, arg2=None, step=None, num_stages=None, loop_unroll_factor=None,
+                 disallow_acc_multi_buffer=False, flatten=False, warp_specialize=False):
         raise RuntimeError("tl.range can only be used in a kernel `for` loop")
 
 

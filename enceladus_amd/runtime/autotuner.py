@@ -38,18 +38,36 @@ FINALIST_BAND = 0.10   # ... when within this fraction of the phase-1 best
 FINAL_ROUNDS = 3
 
 
+DOT_BACKENDS = ("auto", "simdgroup", "mpp")
+
+
 class Config:
-    def __init__(self, kwargs: dict, num_warps: int = 4, num_stages=None, dot_warps=None,
+    """One candidate configuration: constexpr values plus launch options (reference:
+    runtime/autotuner.py:54-103, same fields in the same positional order).
+
+    Args:
+        kwargs: Constexpr values, for example `{"BM": 64, "BN": 64, "BK": 32}`.
+        num_warps: Waves (64 lanes each) per program.
+        dot_warps: The (WM, WN) grid of waves for `tl.dot`, or None for the default.
+        dot_backend: "auto", "simdgroup" or "mpp"; checked, and every `tl.dot` lowers to
+            MFMA on MI355X whichever is named.
+        pre_hook: Called with the bound arguments before each launch of this config.
+    """
+
+    def __init__(self, kwargs: dict, num_warps: int = 4, dot_warps=None,
                  dot_backend: str = "auto", pre_hook: Callable | None = None):
+        if dot_backend not in DOT_BACKENDS:
+            raise ValueError(f"dot_backend must be 'auto', 'simdgroup', or 'mpp', not "
+                             f"{dot_backend!r}")
         self.kwargs = dict(kwargs)
         self.num_warps = num_warps
-        self.num_stages = num_stages
-        self.dot_warps = tuple(dot_warps) if dot_warps else None
+        self.dot_warps = tuple(dot_warps) if dot_warps is not None else None
         self.dot_backend = dot_backend
         self.pre_hook = pre_hook
 
     def _key(self):
-        return (tuple(sorted(self.kwargs.items())), self.num_warps, self.dot_warps)
+        return (tuple(sorted(self.kwargs.items())), self.num_warps, self.dot_warps,
+                self.dot_backend)
 
     def __eq__(self, other):
         return isinstance(other, Config) and self._key() == other._key()
@@ -59,21 +77,36 @@ class Config:
 
     def __repr__(self):
         kw = ", ".join(f"{k}={v}" for k, v in self.kwargs.items())
-        return f"Config({kw}, num_warps={self.num_warps}, dot_warps={self.dot_warps})"
+        tail = f", dot_backend={self.dot_backend!r}" if self.dot_backend != "auto" else ""
+        return f"Config({kw}, num_warps={self.num_warps}, dot_warps={self.dot_warps}{tail})"
+
+    def __str__(self):
+        parts = [repr(self.kwargs), f"num_warps={self.num_warps}"]
+        if self.dot_warps is not None:
+            parts.append(f"dot_warps={self.dot_warps}")
+        if self.dot_backend != "auto":
+            parts.append(f"dot_backend={self.dot_backend!r}")
+        return f"enceladus.Config({', '.join(parts)})"
 
     def launch_options(self) -> dict:
         out = {"num_warps": self.num_warps}
-        if self.dot_warps:
+        if self.dot_warps is not None:
             out["dot_warps"] = self.dot_warps
+        if self.dot_backend != "auto":
+            out["dot_backend"] = self.dot_backend
         return out
 
     def to_json(self) -> dict:
+        """The fields that identify this config (`pre_hook` cannot be serialised)."""
         return {"kwargs": self.kwargs, "num_warps": self.num_warps,
-                "dot_warps": list(self.dot_warps) if self.dot_warps else None}
+                "dot_warps": list(self.dot_warps) if self.dot_warps else None,
+                "dot_backend": self.dot_backend}
 
-    @staticmethod
-    def from_json(d: dict) -> "Config":
-        return Config(dict(d["kwargs"]), int(d["num_warps"]), dot_warps=d.get("dot_warps"))
+    @classmethod
+    def from_json(cls, d: dict) -> "Config":
+        dw = d.get("dot_warps")
+        return cls(dict(d["kwargs"]), int(d["num_warps"]), tuple(dw) if dw else None,
+                   d.get("dot_backend", "auto"))
 
 
 def _jit_of(fn):
@@ -114,7 +147,8 @@ _DTYPE_NAMES = {"float16", "float32", "bfloat16", "int8", "int16", "int32", "int
 
 
 def _compiler_hash() -> str:
-    """Changes whenever the code generator, the device templates or the runtime change."""
+    """Changes whenever any Python source of the package, the device headers or the HIP
+    runtime change (`speccache.compiler_hash`)."""
     from enceladus_amd.runtime.speccache import compiler_hash
     return compiler_hash()
 
@@ -355,7 +389,7 @@ class Autotuner:
 
         def bench(i, warmup_ms, rep, mode):
             try:
-                return do_bench(lambda: launch(cfgs[i]), warmup=warmup_ms, rep=rep,
+                return do_bench(lambda: launch(cfgs[i]), warmup_ms=warmup_ms, rep=rep,
                                 return_mode=mode)
             except Exception as e:  # noqa: BLE001 - a config that fails to launch is skipped
                 errors[i] = e

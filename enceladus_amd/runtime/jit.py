@@ -39,8 +39,9 @@ def _debug() -> bool:
     return os.environ.get("ENCELADUS_DEBUG", "") not in ("", "0")
 
 
-def cdiv(x: int, y: int) -> int:
-    return (x + y - 1) // y
+def cdiv(x: int, div: int) -> int:
+    """`ceil(x / div)` for positive integers: the number of blocks that cover `x`."""
+    return (x + div - 1) // div
 
 
 def next_power_of_2(n: int) -> int:
@@ -357,6 +358,21 @@ class Launcher:
                                            (int(rec[2]), int(rec[3]), int(rec[4])))
 
 
+def _const_canon(v):
+    """A constexpr value as a key: type names and float bit patterns, recursively, so
+    0.0 and -0.0 give different kernels, one NaN launch reuses another's kernel, and
+    `2`, `2.0` and `True` (alone or inside tuples) stay apart. Raises TypeError for an
+    unhashable value."""
+    if isinstance(v, core.dtype):
+        return ("dt", v.name)
+    if isinstance(v, (list, tuple)):
+        return (type(v).__name__,) + tuple(_const_canon(x) for x in v)
+    if isinstance(v, float):
+        return ("float", struct.pack("<d", v))
+    hash(v)
+    return (type(v).__name__, v)
+
+
 # Float math modes (reference: runtime/jit.py:56). "relaxed" (the default) multiplies by
 # the reciprocal of a broadcast row statistic instead of dividing by it; "fast" does so for
 # every divisor that is uniform along the divided tile, scalars included.
@@ -368,8 +384,8 @@ class JITFunction:
 
     _ek_jit = True
 
-    def __init__(self, fn: Callable, do_not_specialize=(), math_mode: str = "relaxed",
-                 interpret=None):
+    def __init__(self, fn: Callable, *, interpret=None, do_not_specialize=(),
+                 math_mode: str = "relaxed"):
         if math_mode not in MATH_MODES:
             raise ValueError(f"math_mode must be one of {MATH_MODES}, but got {math_mode!r}")
         self.fn = fn
@@ -419,10 +435,17 @@ class JITFunction:
                 vals[p.name] = p.default
         return vals
 
-    def specialize(self, vals: dict):
+    def bind(self, args, kwargs):
+        """Binds launch arguments to parameter names, applying defaults (reference:
+        runtime/jit.py:349)."""
+        return self._bind(tuple(args), dict(kwargs))
+
+    def specialize(self, bound: dict):
+        """Argument types, specialization facts and constexpr values of bound arguments
+        (reference: runtime/jit.py:358)."""
         types, facts, consts = {}, {}, {}
         for p in self.params:
-            v = vals[p.name]
+            v = bound[p.name]
             if p.is_constexpr:
                 c = core.unwrap(v)
                 try:
@@ -444,32 +467,28 @@ class JITFunction:
         return types, facts, consts
 
     def _key(self, types, facts, consts, num_warps, dot_warps):
-        def ck(v):
-            if isinstance(v, core.dtype):
-                return ("dt", v.name)
-            if isinstance(v, (list, tuple)):
-                return (type(v).__name__,) + tuple(ck(x) for x in v)
-            if isinstance(v, float):
-                # by bit pattern: 0.0 and -0.0 give different kernels, and one NaN
-                # launch reuses another's kernel
-                return ("float", struct.pack("<d", v))
-            return (type(v).__name__, v)
         return (tuple((k, str(t)) for k, t in types.items()),
                 tuple((k, tuple(sorted(f.items()))) for k, f in facts.items()),
-                tuple((k, ck(v)) for k, v in consts.items()), num_warps,
+                tuple((k, _const_canon(v)) for k, v in consts.items()), num_warps,
                 tuple(dot_warps) if dot_warps else None)
 
-    def _compile_for(self, types, facts, consts, num_warps, dot_warps) -> Launcher:
+    def _options(self, dot_warps) -> dict:
+        """The compile options of a specialization: the same for launches, `warmup`, `ir`
+        and `explain`, so each describes the kernel a launch runs."""
         options = {"dot_warps": tuple(dot_warps) if dot_warps else None,
                    "math_mode": self.math_mode}
         # ENCELADUS_CODEGEN="flag,flag=value": emitter switches for experiments (e.g.
-        # no_staging, no_gemm_template, coarsen); part of the specialization key below.
+        # no_staging, no_gemm_template, coarsen); part of the specialization key.
         for item in filter(None, os.environ.get("ENCELADUS_CODEGEN", "").split(",")):
             k, _, v = item.partition("=")
             v = v.strip()
             options[k.strip()] = int(v) if v.isdigit() else (v if v else True)
-        # ENCELADUS_DEBUG=1 keeps tl.device_assert checks (part of the key below)
+        # ENCELADUS_DEBUG=1 keeps tl.device_assert checks (part of the key)
         options["debug"] = _debug()
+        return options
+
+    def _compile_for(self, types, facts, consts, num_warps, dot_warps) -> Launcher:
+        options = self._options(dot_warps)
         # a specialization an earlier process compiled skips the frontend and codegen
         plain = not (os.environ.get("ENCELADUS_OVERRIDE_DIR") or
                      os.environ.get("ENCELADUS_DUMP", "0") not in ("", "0"))
@@ -503,6 +522,8 @@ class JITFunction:
     def _fast_key(self, args, kwargs, num_warps, dot_warps):
         """(key, runtime values) for the warm path, or None when an argument needs the
         general path (NumPy arrays, unknown or missing arguments, unhashable constexprs)."""
+        if len(args) > len(self.params):
+            return None                 # the general path raises the TypeError
         for k in kwargs:
             if k not in self._name_set:
                 return None
@@ -528,11 +549,15 @@ class JITFunction:
                     key.append((tc, struct.pack("<d", c)))
                 elif tc in (int, bool, str) or isinstance(c, core.dtype):
                     key.append((tc, c))
-                else:
+                elif tc in (tuple, list):
+                    # element types and float bit patterns, as the general key has them:
+                    # (1,), (1.0,) and (True,) are different kernels
                     try:
-                        key.append((tc, hash(c), c))
+                        key.append(_const_canon(c))
                     except TypeError:
                         return None
+                else:
+                    return None
                 continue
             if t is int:
                 key.append((int, v & 15 == 0, v == 1, _int_class(v)))
@@ -571,6 +596,8 @@ class JITFunction:
         same key tuple, the same runtime values) or None when an argument has another type
         (then `_fast_key` runs). Generated once per shape, it replaces the per-parameter
         dispatch of `_fast_key` with straight-line code."""
+        if nargs > len(self.params):
+            return lambda *_: None      # the general path raises the TypeError
         torch = _torch()
         ns = {"_env": _env_token, "_ic": _int_class, "_sc": _span_class, "_li": _last_index,
               "_unwrap": core.unwrap, "_pack": struct.pack, "_dtype": core.dtype,
@@ -673,6 +700,12 @@ class JITFunction:
 
     def run(self, *args, grid, num_warps: int = 4, num_stages=None, dot_warps=None,
             dot_backend: str = "auto", stream=None, **kwargs):
+        """Launches the kernel (reference: runtime/jit.py:388). `num_stages` is accepted for
+        Triton compatibility and has no effect; `dot_backend` ("auto", "simdgroup", "mpp")
+        is checked and every `tl.dot` lowers to MFMA; `stream` (a HIP stream handle)
+        defaults to torch's current stream."""
+        if dot_backend != "auto":
+            check_dot_backend(dot_backend)
         fk = None
         if not self.interpret:
             shape = (len(args), tuple(kwargs))
@@ -717,39 +750,66 @@ class JITFunction:
                     self._fast.pop(fk[0], None)
         return lc.ck
 
-    def warmup(self, *args, num_warps: int = 4, dot_warps=None, grid=None, **kwargs):
+    def warmup(self, *args, grid=None, num_warps: int = 4, dot_warps=None,
+               dot_backend: str = "auto", _record: bool = True, **kwargs):
+        """Compiles the kernel for these arguments without launching it and returns the
+        `CompiledKernel` (`.hip`, `.ir`, `.lds_bytes`, `.num_warps`; reference:
+        runtime/jit.py:527). `dot_backend` is checked and otherwise has no effect: every
+        `tl.dot` lowers to MFMA."""
+        check_dot_backend(dot_backend)
         vals = self._bind(args, kwargs)
         return self._lookup(vals, num_warps, dot_warps).ck
 
-    def ir_for(self, *args, num_warps: int = 4, dot_warps=None, **kwargs) -> ir.Func:
+    def ir(self, *args, num_warps: int = 4, dot_warps=None, **kwargs) -> ir.Func:
+        """The verified IR of the specialization these arguments select, after the pass
+        pipeline, without compiling or launching (reference: runtime/jit.py:378)."""
         vals = self._bind(args, kwargs)
         types, facts, consts = self.specialize(vals)
-        return C.build_module(self, types, facts, consts, num_warps,
-                              {"dot_warps": tuple(dot_warps) if dot_warps else None,
-                               "debug": _debug()})
+        return C.build_module(self, types, facts, consts, num_warps, self._options(dot_warps))
 
-    def explain(self, *args, grid=None, full: bool = False, **kwargs) -> str:
-        """A report of the compiler's decisions for the specialization these arguments
-        select (reference: runtime/jit.py:539): MFMA plans, layout conversions and LDS
-        by source line. `full=True` appends the IR and the generated HIP."""
+    ir_for = ir
+
+    def explain(self, *args, grid=None, num_warps: int = 4, dot_warps=None,
+                dot_backend: str = "auto", full: bool = False, **kwargs) -> str:
+        """Prints and returns a report of the compiler's decisions for the specialization
+        these arguments select (reference: runtime/jit.py:539): MFMA plans, layout
+        conversions and LDS by source line. `full=True` appends the IR and the generated
+        HIP."""
         from enceladus_amd.compiler import codegen_hip
         from enceladus_amd.compiler import explain as EX
-        ck = self.warmup(*args, **kwargs)
+        ck = self.warmup(*args, num_warps=num_warps, dot_warps=dot_warps,
+                         dot_backend=dot_backend, **kwargs)
         if ck.gen.report is None:
-            # loaded from the specialization cache: regenerate the emitter's report
-            nw, dw = kwargs.get("num_warps", 4), kwargs.get("dot_warps")
-            fn_ir = self.ir_for(*args, **kwargs)
-            ck.gen.report = codegen_hip.generate(
-                fn_ir, {"dot_warps": tuple(dw) if dw else None, "debug": _debug()}).report
+            # loaded from the specialization cache: regenerate the emitter's report with
+            # the options the loaded kernel was compiled with
+            fn_ir = self.ir(*args, num_warps=num_warps, dot_warps=dot_warps, **kwargs)
+            ck.gen.report = codegen_hip.generate(fn_ir, self._options(dot_warps)).report
+        if grid is not None and not callable(grid):
+            grid = tuple(grid) if isinstance(grid, (tuple, list)) else (grid,)
+        elif callable(grid):
+            grid = tuple(grid(dict(self._bind(args, kwargs))))
         text = EX.explain(ck, grid)
         if full:
             text += f"\n\n--- IR ---\n{ck.ir}\n--- HIP ---\n{ck.hip}"
+        print(text)
         return text
+
+
+DOT_BACKENDS = ("auto", "simdgroup", "mpp")
+
+
+def check_dot_backend(backend: str) -> str:
+    """The reference's `tl.dot` backend names (runtime/dot_backend.py:108-116). On MI355X
+    every backend lowers to MFMA; an unknown name raises ValueError as there."""
+    if backend not in DOT_BACKENDS:
+        raise ValueError(f"dot_backend must be one of {DOT_BACKENDS}, not {backend!r}")
+    return backend
 
 
 def jit(fn=None, *, interpret=None, do_not_specialize=(), math_mode: str = "relaxed"):
     def deco(f):
-        return JITFunction(f, do_not_specialize, math_mode, interpret)
+        return JITFunction(f, interpret=interpret, do_not_specialize=do_not_specialize,
+                           math_mode=math_mode)
     if fn is not None:
         return deco(fn)
     return deco

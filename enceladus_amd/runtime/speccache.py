@@ -27,6 +27,7 @@ import os
 import struct
 import sys
 import threading
+import weakref
 from pathlib import Path
 
 from enceladus_amd.compiler import codegen_hip
@@ -35,22 +36,37 @@ from enceladus_amd.language import core
 log = logging.getLogger("enceladus")
 
 _lock = threading.Lock()
-_src_hash: dict[int, str] = {}
+# function -> (its code object, hash of its source); weak keys, so a collected function's
+# entry goes with it and a new function can never inherit it
+_src_hash: "weakref.WeakKeyDictionary" = weakref.WeakKeyDictionary()
 _COMPILER = None
 
 
+def hashed_sources(root: Path | None = None) -> list[Path]:
+    """Every file whose text decides generated code or launch metadata: all Python sources
+    of the package (frontend, passes, emitter, and the runtime's pass pipeline, argument
+    facts and specialization rules) and the device headers."""
+    root = root or Path(__file__).resolve().parent.parent
+    files = [p for p in root.rglob("*.py") if "__pycache__" not in p.parts]
+    files += list((root / "csrc" / "include").glob("*.h"))
+    return sorted(files, key=lambda p: p.relative_to(root).as_posix())
+
+
+def tree_hash(root: Path) -> "hashlib._Hash":
+    """sha256 over the names and bytes of `hashed_sources(root)`."""
+    h = hashlib.sha256()
+    for p in hashed_sources(root):
+        h.update(p.relative_to(root).as_posix().encode())
+        h.update(p.read_bytes())
+    return h
+
+
 def compiler_hash() -> str:
-    """Changes whenever the code generator, the device headers or the HIP runtime change."""
+    """Changes whenever any Python source of the package, the device headers or the HIP
+    runtime change."""
     global _COMPILER
     if _COMPILER is None:
-        root = Path(__file__).resolve().parent.parent
-        h = hashlib.sha256()
-        for sub in ("compiler", "language", os.path.join("csrc", "include")):
-            d = root / sub
-            for p in sorted(d.iterdir()):
-                if p.suffix in (".py", ".h"):
-                    h.update(p.name.encode())
-                    h.update(p.read_bytes())
+        h = tree_hash(Path(__file__).resolve().parent.parent)
         try:
             from enceladus_amd.runtime import hip
             lib = hip.load_library()
@@ -64,15 +80,22 @@ def compiler_hash() -> str:
 
 
 def _source_hash(fn) -> str | None:
-    k = id(fn)
-    h = _src_hash.get(k)
-    if h is None:
-        try:
-            src = inspect.getsource(fn)
-        except (OSError, TypeError):
-            return None
-        h = hashlib.sha256(src.encode()).hexdigest()[:24]
-        _src_hash[k] = h
+    code = getattr(fn, "__code__", None)
+    try:
+        hit = _src_hash.get(fn)
+    except TypeError:                   # not weak-referenceable: hash it every time
+        hit = None
+    if hit is not None and hit[0] is code:
+        return hit[1]
+    try:
+        src = inspect.getsource(fn)
+    except (OSError, TypeError):
+        return None
+    h = hashlib.sha256(src.encode()).hexdigest()[:24]
+    try:
+        _src_hash[fn] = (code, h)
+    except TypeError:
+        pass
     return h
 
 

@@ -231,36 +231,36 @@ def _shape_arg(shape) -> tuple:
     return tuple(int(s) for s in shape)
 
 
-def empty(shape, dtype=core.float32) -> Tensor:
+def empty(shape, dtype="float32") -> Tensor:
     if isinstance(shape, int):
         shape = (shape,)
     return Tensor(shape, _as_dtype(dtype))
 
 
-def full(shape, value, dtype=core.float32) -> Tensor:
+def full(shape, value, dtype="float32") -> Tensor:
     """A tensor filled with `value` (reference: runtime/tensor.py:290-302)."""
     if isinstance(shape, int):
         shape = (shape,)
     dt = _as_dtype(dtype)
-    return from_numpy(np.full(tuple(shape), value, dt.to_numpy()), dt)
+    return from_numpy(np.full(tuple(shape), value, dt.to_numpy()), dtype=dt)
 
 
-def ones(shape, dtype=core.float32) -> Tensor:
+def ones(shape, dtype="float32") -> Tensor:
     return full(shape, 1, dtype)
 
 
-def rand(*shape, dtype=core.float32, seed: int | None = None) -> Tensor:
+def rand(*shape, dtype="float32", seed: int | None = None) -> Tensor:
     """Samples from the uniform distribution on [0, 1) (reference: tensor.py:316-321)."""
     shape = _shape_arg(shape)
     v = np.random.default_rng(seed).random(shape, dtype=np.float32)
-    return from_numpy(v.astype(_as_dtype(dtype).to_numpy()), dtype)
+    return from_numpy(v.astype(_as_dtype(dtype).to_numpy()), dtype=dtype)
 
 
-def arange(start: int, end: int | None = None, step: int = 1, dtype=core.int32) -> Tensor:
+def arange(start: int, end: int | None = None, step: int = 1, dtype="int32") -> Tensor:
     if end is None:
         start, end = 0, start
     dt = _as_dtype(dtype)
-    return from_numpy(np.arange(start, end, step).astype(dt.to_numpy()), dt)
+    return from_numpy(np.arange(start, end, step).astype(dt.to_numpy()), dtype=dt)
 
 
 def empty_like(t: Any, dtype=None) -> Tensor:
@@ -271,7 +271,7 @@ def zeros_like(t: Any, dtype=None) -> Tensor:
     return zeros(tuple(t.shape), dtype if dtype is not None else elem_dtype(t))
 
 
-def zeros(shape, dtype=core.float32) -> Tensor:
+def zeros(shape, dtype="float32") -> Tensor:
     t = empty(shape, dtype)
     if t.nbytes:
         hip.call("ek_memset", ctypes.c_void_p(t.ptr), 0, t.nbytes, None)
@@ -279,17 +279,19 @@ def zeros(shape, dtype=core.float32) -> Tensor:
     return t
 
 
-def from_numpy(a: np.ndarray, dtype=None) -> Tensor:
+def from_numpy(a: np.ndarray, *, dtype=None) -> Tensor:
+    """A device tensor holding a copy of `a` (HBM is not host-visible, so it never aliases
+    `a`); `dtype` reinterprets the elements' storage, e.g. uint16 data as bfloat16."""
     dt = _as_dtype(dtype) if dtype is not None else core.dtype_from_numpy(a.dtype)
     t = Tensor(a.shape, dt)
     return t.copy_from_numpy(a)
 
 
-def randn(*shape, dtype=core.float32, seed: int | None = None) -> Tensor:
+def randn(*shape, dtype="float32", seed: int | None = None) -> Tensor:
     """Samples from the standard normal distribution (reference: tensor.py:308-313)."""
     rng = np.random.default_rng(seed)
     return from_numpy(rng.standard_normal(_shape_arg(shape), dtype=np.float32).astype(
-        _as_dtype(dtype).to_numpy()), dtype)
+        _as_dtype(dtype).to_numpy()), dtype=dtype)
 
 
 def _as_dtype(dt) -> core.dtype:
@@ -309,14 +311,14 @@ def _is_torch(x: Any) -> bool:
     return t is not None and isinstance(x, t.Tensor)
 
 
-def element_dtype(x: Any) -> np.dtype:
-    """The NumPy dtype of `x`'s elements; bfloat16 reports `core.BF16_TAG` (kind "V")."""
-    if isinstance(x, Tensor):
-        dt = x.dtype
-    elif _is_torch(x):
-        dt = core.dtype_from_torch(x.dtype)
+def element_dtype(obj: Any) -> np.dtype:
+    """The NumPy dtype of `obj`'s elements; bfloat16 reports `core.BF16_TAG` (kind "V")."""
+    if isinstance(obj, Tensor):
+        dt = obj.dtype
+    elif _is_torch(obj):
+        dt = core.dtype_from_torch(obj.dtype)
     else:
-        return np.asarray(x).dtype
+        return np.asarray(obj).dtype
     return core.BF16_TAG if dt is core.bfloat16 else dt.to_numpy()
 
 
@@ -328,35 +330,38 @@ def elem_dtype(x: Any) -> core.dtype:
     return core.dtype_from_numpy(np.asarray(x).dtype)
 
 
-def element_strides(x: Any) -> tuple[int, ...]:
-    if isinstance(x, Tensor):
-        return x.strides
-    if _is_torch(x):
-        return tuple(x.stride())
-    a = np.asarray(x)
+def element_strides(obj: Any) -> tuple[int, ...]:
+    """The strides of any supported array, in elements."""
+    if isinstance(obj, Tensor):
+        return obj.strides
+    if _is_torch(obj):
+        return tuple(obj.stride())
+    a = np.asarray(obj)
     return tuple(s // a.itemsize for s in a.strides)
 
 
-def new_empty(x: Any, shape=None, dtype=None):
-    shape = tuple(x.shape) if shape is None else tuple(shape)
-    if _is_torch(x):
+def new_empty(like: Any, shape=None, dtype=None):
+    """An uninitialised array of `like`'s kind (NumPy, torch, Tensor) and device."""
+    shape = tuple(like.shape) if shape is None else tuple(shape)
+    if _is_torch(like):
         import torch
-        tdt = x.dtype if dtype is None else _torch_dtype(dtype)
-        return torch.empty(shape, dtype=tdt, device=x.device)
-    if isinstance(x, Tensor):
-        return empty(shape, x.dtype if dtype is None else _as_dtype(dtype))
-    return np.empty(shape, _numpy_storage(np.asarray(x).dtype if dtype is None else dtype))
+        tdt = like.dtype if dtype is None else _torch_dtype(dtype)
+        return torch.empty(shape, dtype=tdt, device=like.device)
+    if isinstance(like, Tensor):
+        return empty(shape, like.dtype if dtype is None else _as_dtype(dtype))
+    return np.empty(shape, _numpy_storage(np.asarray(like).dtype if dtype is None else dtype))
 
 
-def new_zeros(x: Any, shape=None, dtype=None):
-    shape = tuple(x.shape) if shape is None else tuple(shape)
-    if _is_torch(x):
+def new_zeros(like: Any, shape=None, dtype=None):
+    """A zero-filled array of `like`'s kind (NumPy, torch, Tensor) and device."""
+    shape = tuple(like.shape) if shape is None else tuple(shape)
+    if _is_torch(like):
         import torch
-        tdt = x.dtype if dtype is None else _torch_dtype(dtype)
-        return torch.zeros(shape, dtype=tdt, device=x.device)
-    if isinstance(x, Tensor):
-        return zeros(shape, x.dtype if dtype is None else _as_dtype(dtype))
-    return np.zeros(shape, _numpy_storage(np.asarray(x).dtype if dtype is None else dtype))
+        tdt = like.dtype if dtype is None else _torch_dtype(dtype)
+        return torch.zeros(shape, dtype=tdt, device=like.device)
+    if isinstance(like, Tensor):
+        return zeros(shape, like.dtype if dtype is None else _as_dtype(dtype))
+    return np.zeros(shape, _numpy_storage(np.asarray(like).dtype if dtype is None else dtype))
 
 
 def _numpy_storage(dt) -> np.dtype:

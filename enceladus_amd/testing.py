@@ -1,8 +1,10 @@
 """Benchmark and comparison helpers (reference: src/enceladus/testing.py:14-90).
 
-`do_bench` times a callable with HIP events recorded on the launch stream: warm up for
-`warmup` ms, then `rep` timed repetitions; returns the median (or the requested
-statistic) in ms.
+`do_bench` times a callable on the GPU: it warms up until `warmup_ms` of GPU time has been
+spent, then takes `rep` timed samples and returns their median (or the requested
+statistic) in ms. `default_tolerance` and `assert_close` give the reference's public
+dtype tolerances. (The test suite's own differential table, which is tighter for fp16 and
+bf16, lives in `tests/conftest.py`.)
 """
 
 from __future__ import annotations
@@ -15,22 +17,34 @@ import numpy as np
 from enceladus_amd.runtime import device as D
 from enceladus_amd.runtime import hip
 
-_TOL = {"float32": (1e-5, 1e-5), "float16": (1e-3, 2e-3), "bfloat16": (1e-2, 1.6e-2)}
-
 
 def default_tolerance(dtype) -> tuple[float, float]:
-    name = getattr(dtype, "long_name", None) or np.dtype(dtype).name
-    return _TOL.get(name, (0.0, 0.0))
+    """(atol, rtol) suited to comparing results of `dtype` (reference: testing.py:66-75)."""
+    name = getattr(dtype, "long_name", None)
+    if name is None:
+        if hasattr(dtype, "to_numpy"):
+            dtype = dtype.to_numpy()
+        dt = np.dtype(dtype)
+        name = "bfloat16" if dt.kind == "V" and dt.itemsize == 2 else dt.name
+    if name == "bfloat16":
+        return 2e-2, 2e-2
+    if name == "float16":
+        return 2e-3, 2e-3
+    if name == "float32":
+        return 1e-5, 1e-5
+    return 0.0, 0.0
 
 
-def assert_close(actual, expected, atol=None, rtol=None, dtype=None):
-    a = np.asarray(actual, np.float64)
-    e = np.asarray(expected, np.float64)
-    if atol is None or rtol is None:
-        ta, tr = default_tolerance(dtype or np.asarray(expected).dtype)
-        atol = ta if atol is None else atol
-        rtol = tr if rtol is None else rtol
-    np.testing.assert_allclose(a, e, atol=atol, rtol=rtol)
+def assert_close(actual, expected, atol=None, rtol=None, *, dtype=None):
+    """Asserts that two arrays match within tolerances chosen from `actual`'s dtype (or
+    `dtype`) unless given (reference: testing.py:80-90)."""
+    a = np.asarray(actual)
+    e = np.asarray(expected)
+    d_atol, d_rtol = default_tolerance(dtype if dtype is not None else a.dtype)
+    np.testing.assert_allclose(
+        a.astype(np.float64) if a.dtype.kind in "fV" else a,
+        e.astype(np.float64) if e.dtype.kind in "fV" else e,
+        atol=d_atol if atol is None else atol, rtol=d_rtol if rtol is None else rtol)
 
 
 class _Events:
@@ -56,14 +70,27 @@ class _Events:
         return ms.value
 
 
-def do_bench(fn, warmup: float = 50, rep: int = 20, return_mode: str = "median",
+def do_bench(fn, warmup_ms: float = 50.0, rep: int = 20, return_mode: str = "median", *,
              stream: int | None = None):
-    """Times `fn` on the GPU in ms. Each sample is the GPU time of the dispatches `fn`
-    launches through this runtime, from the first one's start to the last one's end
-    (`runtime.timing.DispatchTimer`), so host launch latency is excluded; an `fn` that
-    launches nothing through the runtime (a torch op) is timed with events around it."""
+    """Times `fn` on the GPU and returns milliseconds (reference: testing.py:14-63).
+
+    Each sample is the GPU time of the dispatches `fn` launches through this runtime, from
+    the first one's start to the last one's end (`runtime.timing.DispatchTimer`), so host
+    launch latency is excluded; an `fn` that launches nothing through the runtime (a torch
+    op) is timed with HIP events around it on `stream` (torch's current stream by
+    default). Before sampling, `fn` runs until `warmup_ms` of GPU time has been spent:
+    the clock is low after an idle spell, so cold samples run slow.
+
+    Args:
+        fn: A function that launches one or more kernels.
+        warmup_ms: GPU time to spend warming up before measuring.
+        rep: The number of timed repetitions.
+        return_mode: "median", "min", "mean", or "all" (a list of every sample).
+    """
     from enceladus_amd.runtime.timing import DispatchTimer
-    fn()
+    if return_mode not in ("median", "min", "mean", "all"):
+        raise ValueError(f"return_mode must be 'median', 'min', 'mean' or 'all', not "
+                         f"{return_mode!r}")
     D.synchronize()
     ev = _Events()
     timer = DispatchTimer()
@@ -76,11 +103,13 @@ def do_bench(fn, warmup: float = 50, rep: int = 20, return_mode: str = "median",
             return timer.ms()
         return ev.time(fn, s)
 
-    first = sample()
-    n_warm = max(1, int(warmup / max(first, 1e-3)))
-    for _ in range(min(n_warm, 1000)):
-        fn()
-    D.synchronize()
+    spent = 0.0
+    while spent < warmup_ms:
+        t = sample()
+        if t <= 0.0:
+            raise RuntimeError("do_bench measured no GPU work; fn must launch kernels on the "
+                               "GPU")
+        spent += t
     times = [sample() for _ in range(rep)]
     if return_mode == "all":
         return times

@@ -215,6 +215,6 @@ def test_do_bench_times_dispatches_not_host_latency():
     def slow_host():
         time.sleep(0.002)
         _scale[(n // 1024,)](x, out, n, 2.0, BLOCK=1024)
-    ms = do_bench(slow_host, warmup=1, rep=5)
+    ms = do_bench(slow_host, warmup_ms=1, rep=5)
     assert ms < 1.0, ms                 # a 4 MB scale takes microseconds, not the 2 ms sleep
     torch.testing.assert_close(out, x * 2.0)

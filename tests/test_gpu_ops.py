@@ -178,6 +178,26 @@ def test_int_ops(op, dtype):
     np.testing.assert_array_equal(got, want)
 
 
+@pytest.mark.parametrize("dtype", [np.int8, np.int16, np.int32, np.int64, np.uint8, np.uint32])
+@pytest.mark.parametrize("op", ["shl", "shr"])
+def test_shift_counts_out_of_range(op, dtype):
+    """Counts that are negative or at least the bit width follow NumPy's shift rules, as
+    the reference interpreter's `np.left_shift`/`np.right_shift` do (reference
+    interpreter/interp.py:622-623): a left shift gives 0, a right shift the sign fill.
+    Checked against NumPy itself as well as the oracle; counts into the sign bit wrap."""
+    _say(f"shift {op} out of range {np.dtype(dtype).name}")
+    rng = np.random.default_rng(11)
+    info = np.iinfo(dtype)
+    x = rng.integers(info.min, info.max, N, endpoint=True, dtype=dtype)
+    counts = np.concatenate([np.arange(-70, 140), [info.bits - 1, info.bits, info.bits + 1,
+                                                     2 * info.bits, 255, 256, 257]])
+    y = np.resize(counts, N).astype(np.int64).astype(dtype)     # wraps as the cast does
+    got, want = _run_both(_binary_kernel, (4,), (x, y), dtype, OP=op, BLOCK=256)
+    np.testing.assert_array_equal(got, want)
+    ref = np.left_shift(x, y) if op == "shl" else np.right_shift(x, y)
+    np.testing.assert_array_equal(got, ref)
+
+
 @enceladus.jit
 def _cast_kernel(x_ptr, out_ptr, n, BLOCK: tl.constexpr):
     offs = tl.program_id(0) * BLOCK + tl.arange(0, BLOCK)

@@ -162,3 +162,115 @@ def test_gelu_closed_form():
     O.run_grid(fused_gelu_kernel, (1,), x, bias, out, 240, 30, 0.5, BLOCK=256)
     np.testing.assert_allclose(out, R.fused_gelu(x, bias, 0.5), rtol=1e-5, atol=1e-6)
     assert math.isclose(float(R.gelu64(np.array([1.0]))[0]), 0.8413447460685429, rel_tol=1e-12)
+
+
+# -- math functions at points the mathematics fixes -----------------------------------
+# Each value is exact in float32 (or the function's correctly rounded result is), so a
+# swapped function (sin for cos, log for log2, tanh for sigmoid), a dropped sign or a
+# wrong base fails here.
+
+def _un(op, vals):
+    return O.unary(op, O.to_tile(np.array(vals, np.float32))).data.tolist()
+
+
+def test_math_functions_at_exact_points():
+    inf, nan = math.inf, math.nan
+    assert _un("sin", [0.0, -0.0]) == [0.0, -0.0]
+    assert math.copysign(1, _un("sin", [-0.0])[0]) == -1
+    assert _un("sin", [np.float32(math.pi / 2)]) == [1.0]
+    assert _un("sin", [np.float32(-math.pi / 2)]) == [-1.0]
+    assert _un("cos", [0.0, -0.0]) == [1.0, 1.0]
+    assert abs(_un("cos", [np.float32(math.pi)])[0] + 1.0) < 1e-7
+    assert _un("tanh", [0.0, inf, -inf, 20.0, -20.0]) == [0.0, 1.0, -1.0, 1.0, -1.0]
+    assert _un("sigmoid", [0.0, inf, -inf, 100.0]) == [0.5, 1.0, 0.0, 1.0]
+    assert _un("log", [1.0, 0.0, inf]) == [0.0, -inf, inf]
+    assert math.isnan(_un("log", [-1.0])[0])
+    assert _un("log2", [1.0, 2.0, 8.0, 0.5, 2.0 ** -20, 2.0 ** 100, 0.0]) == \
+        [0.0, 1.0, 3.0, -1.0, -20.0, 100.0, -inf]
+    assert math.isnan(_un("log2", [-2.0])[0]) and math.isnan(_un("sin", [inf])[0])
+    assert _un("exp2", [0.0, 3.0, -2.0, 10.0]) == [1.0, 8.0, 0.25, 1024.0]
+    assert _un("exp", [0.0, -inf]) == [1.0, 0.0]
+    assert _un("sqrt", [4.0, 0.25, 0.0]) == [2.0, 0.5, 0.0]
+    assert _un("rsqrt", [4.0, 0.25]) == [0.5, 2.0]
+    assert _un("floor", [-2.5, 2.5, -0.0]) == [-3.0, 2.0, -0.0]
+    assert _un("ceil", [-2.5, 2.5]) == [-2.0, 3.0]
+    assert _un("erf", [0.0, inf, -inf]) == [0.0, 1.0, -1.0]
+
+
+def test_math_functions_satisfy_identities():
+    """Identities between functions on random float32 inputs, to float32 tolerance:
+    sin² + cos² = 1, tanh(x) = 2·sigmoid(2x) − 1, log2(x) = log(x) / ln 2,
+    exp(log x) = x, sin(−x) = −sin(x), cos(−x) = cos(x)."""
+    x = np.random.default_rng(3).uniform(-6, 6, 4096).astype(np.float32)
+    p = np.abs(x) + np.float32(0.01)
+    s, c = np.array(_un("sin", x)), np.array(_un("cos", x))
+    np.testing.assert_allclose(s * s + c * c, 1.0, atol=1e-6)
+    np.testing.assert_allclose(_un("tanh", x), 2 * np.array(_un("sigmoid", 2 * x)) - 1,
+                               atol=2e-6)
+    np.testing.assert_allclose(_un("log2", p), np.array(_un("log", p)) / math.log(2),
+                               rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(_un("exp", _un("log", p)), p, rtol=2e-6)
+    assert _un("sin", -x) == [-v for v in _un("sin", x)]
+    assert _un("cos", -x) == _un("cos", x)
+
+
+# -- argmax / argmin: first index of the NaN-ignoring extreme ----------------------------
+
+def _brute_arg(row, kind):
+    """Pure-Python restatement of the rule (reference language/ops.py:962-968): the first
+    index whose value equals the NaN-ignoring max (min); an all-NaN row gives 0."""
+    vals = [v for v in row if not (isinstance(v, float) and math.isnan(v))]
+    if not vals:
+        return 0
+    best = max(vals) if kind == "argmax" else min(vals)
+    return next(i for i, v in enumerate(row) if v == best)
+
+
+def test_argmax_argmin_ties_and_nans():
+    nan = math.nan
+    rows = [[3.0, 1.0, 3.0, 2.0], [nan, 2.0, 5.0, nan], [nan, nan, nan, nan],
+            [1.0, nan, 1.0, 0.5], [-0.0, 0.0, -1.0, -1.0], [-math.inf, -math.inf, nan, 7.0],
+            [2.0, 2.0, 2.0, 2.0], [nan, -3.0, -3.0, 4.0]]
+    a = np.array(rows, np.float32)
+    for kind, fn in (("argmax", O.argmax), ("argmin", O.argmin)):
+        got = fn(O.to_tile(a), 1).data.tolist()
+        want = [_brute_arg([float(v) for v in r], kind) for r in a]
+        assert got == want, kind
+        col = fn(O.to_tile(a.T.copy()), 0).data.tolist()
+        assert col == want
+    # the value tl.max returns and the argmax index agree, NaNs ignored
+    mx = O.max(O.to_tile(a), 1).data
+    idx = O.argmax(O.to_tile(a), 1).data
+    for r, m, i in zip(a, mx, idx):
+        if not np.all(np.isnan(r)):
+            assert r[i] == m
+    ints = np.array([[5, 9, 9, 1], [-4, -4, -9, -9]], np.int32)
+    assert O.argmax(O.to_tile(ints), 1).data.tolist() == [1, 0]
+    assert O.argmin(O.to_tile(ints), 1).data.tolist() == [3, 2]
+
+
+# -- shifts: NumPy's rules, which the reference interpreter inherits ------------------------
+
+@pytest.mark.parametrize("dt", ["int8", "int16", "int32", "int64", "uint8", "uint16",
+                                "uint32", "uint64"])
+def test_shift_counts_follow_numpy(dt):
+    """The reference shifts with `np.left_shift`/`np.right_shift` on counts cast to the
+    value's dtype (interpreter/interp.py:622-623). For every count in [-70, 300) (cast as
+    the compute dtype casts it), the oracle equals NumPy, and the out-of-range rule is the
+    closed form: left shifts give 0, right shifts the sign fill."""
+    npdt = np.dtype(dt)
+    info = np.iinfo(npdt)
+    x = np.array([info.min, info.max, 0, 1, 5, info.min + 3, info.max // 3], npdt)
+    for c in range(-70, 300):
+        y = np.full(x.shape, c, np.int64).astype(npdt)
+        ot = O.to_tile(x)
+        oc = O.to_tile(y)
+        sl = O.binary("shl", ot, oc).data
+        sr = O.binary("shr", ot, oc).data
+        assert np.array_equal(sl, np.left_shift(x, y)), (dt, c)
+        assert np.array_equal(sr, np.right_shift(x, y)), (dt, c)
+        cnt = int(y[0])
+        if cnt < 0 or cnt >= info.bits:
+            assert np.all(sl == 0)
+            fill = np.where(x < 0, -1, 0).astype(npdt) if info.min < 0 else np.zeros_like(x)
+            assert np.array_equal(sr, fill)

@@ -71,3 +71,43 @@ def test_changed_global_or_specialization_compiles_again(tmp_path):
     assert _run(tmp, 3.0)[0] == 1          # SCALE changed: the fingerprint differs
     assert _run(tmp, 3.0)[0] == 0
     assert _run(tmp, 3.0, n=1024)[0] == 1  # n divisible by 16: another specialization
+
+
+def test_compiler_hash_covers_the_runtime_sources(tmp_path):
+    """The pass pipeline (runtime/compile.py) and the argument facts (runtime/jit.py) decide
+    generated code too: editing either changes the hash every persistent key includes."""
+    import shutil
+    from pathlib import Path
+
+    from enceladus_amd.runtime import speccache
+    pkg = Path(speccache.__file__).resolve().parent.parent
+    names = {p.relative_to(pkg).as_posix() for p in speccache.hashed_sources(pkg)}
+    for must in ("runtime/compile.py", "runtime/jit.py", "compiler/codegen_hip.py",
+                 "language/ops.py", "csrc/include/enceladus_cdna4.h"):
+        assert must in names
+    copy = tmp_path / "pkg"
+    shutil.copytree(pkg, copy, ignore=shutil.ignore_patterns("__pycache__", "*.so"))
+    before = speccache.tree_hash(copy).hexdigest()
+    for rel in ("runtime/jit.py", "runtime/compile.py"):
+        f = copy / rel
+        f.write_text(f.read_text() + "\n# edited\n")
+        after = speccache.tree_hash(copy).hexdigest()
+        assert after != before
+        before = after
+
+
+def test_source_hash_is_not_inherited_by_a_new_function():
+    """The source-hash memo holds its functions weakly and checks the code object, so a
+    function created after another was collected never reuses the other's hash."""
+    import gc
+
+    from enceladus_amd.runtime import speccache
+    ns = {}
+    exec("def f():\n    return 1\n", ns)
+    f = ns["f"]
+    assert speccache._source_hash(f) is None        # no source file: nothing cached
+    h = speccache._source_hash(test_source_hash_is_not_inherited_by_a_new_function)
+    assert h == speccache._source_hash(test_source_hash_is_not_inherited_by_a_new_function)
+    del f, ns
+    gc.collect()
+    assert all(k is not None for k in speccache._src_hash.keys())
