@@ -176,9 +176,9 @@ def measure(torch, timer, wl, steps, warmup, pin=None):
     best = None
     for v in choices:
         launches = [make_launch(wl.kernel(), *wl.args(s, v), v.options()) for s in sets]
-        k = steps if wl.bound == "hbm" else max(5, steps // 2)
-        if wl.name == "vector_add" or wl.name.startswith("attention"):
-            k = max(4, steps // 4)
+        # at least 20 timed launches per row (vector add and attention each take about
+        # 0.5 ms a launch, so 20 of them are 10-12 ms of GPU time)
+        k = max(20, steps)
         ms = timer.run(launches, k, max(2, warmup // 2))
         log(f"    {v.label}: {ms * 1e3:.1f} us")
         if best is None or ms < best[0]:
@@ -297,15 +297,37 @@ def tuned_named(tuned, args, fixed):
     return _named(tuned.fn, args, fixed)
 
 
+def source_stamp() -> str:
+    """A hash of everything that decides the generated kernels: the package's Python
+    sources and device headers, and the example kernels and workload table. A counter
+    summary records the stamp of the tree it measured."""
+    import hashlib
+    from pathlib import Path
+
+    from enceladus_amd.runtime import speccache
+    h = speccache.tree_hash(Path(ROOT) / "enceladus_amd")
+    for p in sorted((Path(ROOT) / "examples").glob("*.py")):
+        h.update(p.name.encode())
+        h.update(p.read_bytes())
+    return h.hexdigest()[:16]
+
+
 def measured_traffic(name: str):
     """HBM bytes per launch of workload `name` from the committed rocprofv3 counter
-    summaries (`traffic_bytes_per_launch[name]: N` lines), or None."""
+    summaries (`traffic_bytes_per_launch[name]: N` lines), or None when no summary has
+    the row or the summary measured other sources than this tree's (its
+    `source_stamp: ...` line differs from `source_stamp()`): a stale figure is not
+    reported."""
     import glob
     tag = f"traffic_bytes_per_launch[{name}]:"
+    here = source_stamp()
     for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*counters*.txt"))):
-        for line in open(path).read().splitlines():
+        lines = open(path).read().splitlines()
+        stamp = next((ln.split(":", 1)[1].strip() for ln in lines
+                      if ln.startswith("source_stamp:")), None)
+        for line in lines:
             if line.startswith(tag):
-                return int(line.split(":")[1])
+                return int(line.split(":")[1]) if stamp == here else None
     return None
 
 
@@ -482,7 +504,12 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--pin", default="", help="NAME=INDEX[,NAME=INDEX]: time only that "
                     "variant of the workload's table (profiling runs)")
+    ap.add_argument("--print-stamp", action="store_true", help="print the source stamp "
+                    "that counter summaries record, and exit")
     args = ap.parse_args()
+    if args.print_stamp:
+        print(source_stamp())
+        return
     pins = {k: int(v) for k, v in (p.split("=") for p in args.pin.split(",") if p)}
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; multi-GPU runs are out "
@@ -557,6 +584,7 @@ def main():
                       "peak": MFMA_PEAK_F16 / 1e12, "unit": "TFLOP/s"}) | {
                      "frac": round(head["roofline_frac"], 4),
                      "traffic": head.get("traffic")},
+        "source_stamp": source_stamp(),
         "workloads": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
                           for kk, vv in v.items()} for k, v in results.items()},
     }

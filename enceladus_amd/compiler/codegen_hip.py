@@ -1822,20 +1822,32 @@ class Emitter:
         pv = self.priv.get(res.id) if hasattr(self, "priv") else None
         if pv is not None:
             idx = ptr.op.operands[1]
-            conds = [own] if own else []
+            # Copies of an element replicated over a warp bit sit in whole waves: those
+            # waves skip the atomics with a wave-uniform branch. Over a lane bit, and for
+            # masked-off elements, a lane adds 0 instead, which keeps the loop one basic
+            # block; its dummy address is a bin of its own (its lane number), so the dummy
+            # adds of a wave never pile onto one LDS word (all on bin 0 they serialised:
+            # an 8-wave launch whose upper four waves were copies ran 3x slower).
+            lm = sum(1 << i for i, b in enumerate(lay.lane) if b is None)
+            wm = sum(1 << i for i, b in enumerate(lay.warp) if b is None)
+            conds = [f"((ek_lane & {lm}) == 0)"] if lm else []
             conds.append(f"({self.elem(mask, lay, 'r')})")
             ie = self.elem(idx, lay, "r")
             ve = self.elem(val_v, lay, "r")
             cop = self.priv_copies
-            # Branch-free: a masked-off lane adds 0 to bin 0 (the mask bounds the index, so
-            # an unmasked index is always a valid bin), which keeps the loop one basic block.
-            ie = f"(({' && '.join(conds)}) ? ({ie}) : 0)"
+            bins = pv["bins"]
+            dummy = "ek_lane" if bins >= 64 else f"(ek_lane % {bins})"
+            ie = f"(({' && '.join(conds)}) ? ({ie}) : {dummy})"
             ve = f"(({' && '.join(conds)}) ? ({ve}) : 0)"
             slot = f"{ie} * {cop} + (ek_lane & {cop - 1})" if cop > 1 else ie
+            if wm:
+                self.emit(f"if ((ek_warp & {wm}) == 0) {{")
             self.emit("#pragma unroll")
             self.emit(f"for (int r = 0; r < {lay.nregs}; ++r) "
                       f"__hip_atomic_fetch_add(&{pv['name']}[{slot}], {ve}, "
                       f"__ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);")
+            if wm:
+                self.emit("}")
             self.define(res, "ek_unused")
             return
         nm = self.fresh("at")

@@ -211,11 +211,16 @@ def blocked(shape, order, vec: int, num_warps: int) -> Layout:
     shape = tuple(shape)
     bits = [(d, i) for d in order for i in range(log2(shape[d]))]
     nvec = min(log2(vec), log2(shape[order[0]])) if shape else 0
+    wb = log2(num_warps)
+    if len(bits) >= LANE_BITS + wb:
+        # narrower vectors when the full width would leave threads holding copies: a
+        # 1024-element tile over 8 waves takes 2 elements per thread, not 4 (with 4, the
+        # upper four waves would load the tile a second time)
+        nvec = min(nvec, len(bits) - LANE_BITS - wb)
     reg = bits[:nvec]
     rest = bits[nvec:]
     lane = rest[:LANE_BITS]
     rest = rest[LANE_BITS:]
-    wb = log2(num_warps)
     warp = rest[:wb]
     rest = rest[wb:]
     reg = reg + rest

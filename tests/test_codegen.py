@@ -20,10 +20,22 @@ def test_every_workload_kernel_compiles_for_gfx950():
 def test_codegen_is_deterministic():
     from examples.vector_add import add_kernel
     x = np.zeros(4, np.float32)
-    a = codegen_hip.generate(add_kernel.ir_for(x, x, x, 1000, BLOCK=256)).source
-    b = codegen_hip.generate(add_kernel.ir_for(x, x, x, 1000, BLOCK=256)).source
+    a = codegen_hip.generate(add_kernel.ir_for(x, x, x, 1000, BLOCK=1024)).source
+    b = codegen_hip.generate(add_kernel.ir_for(x, x, x, 1000, BLOCK=1024)).source
     assert a == b
     assert "vload_nt<float, 4>" in a   # 128-bit streaming accesses for aligned contiguous fp32
+
+
+def test_blocked_layout_avoids_copies_when_the_tile_allows():
+    """A tile with at least one element per thread is spread over every thread: the vector
+    narrows instead of leaving waves that hold (and load) copies."""
+    for n, nw, vec in ((1024, 4, 4), (1024, 8, 2), (1024, 16, 1), (256, 4, 1), (8192, 16, 4)):
+        lay = L.default_blocked((n,), nw)
+        assert lay.nregs * 64 * nw == n, (n, nw)
+        assert all(b is not None for b in (*lay.lane, *lay.warp)), (n, nw)
+        assert len([b for b in lay.reg if b[1] < L.log2(vec)]) == L.log2(vec)
+    small = L.default_blocked((64,), 4)          # fewer elements than threads: copies remain
+    assert small.nregs == 4 and any(b is None for b in small.warp)
 
 
 def _covers_once(lay):

@@ -14,7 +14,8 @@ against the CPU oracle (reference protocol: tests/conftest.py:102-145):
 - matmul and matmul + bias + GELU 4096^3: every element against an fp32 product (the
   oracle's `dot` arithmetic) at the fp16 tolerance, plus the oracle itself on sampled
   programs;
-- flash attention bf16 [4,32,4096,128] causal and [4,32,1024,128]: the oracle on a sample of
+- flash attention bf16 [4,32,4096,128] causal and [4,32,1024,128]: every output element
+  against an fp32 reference computed on the GPU, the oracle on a sample of
   (start_m, batch*head) programs stratified over start_m (first, middle, last blocks) and
   the float64 closed form on the same rows;
 - the two copy kernels the benchmark reports as HBM ceilings: bit-exact; the read-only
@@ -278,15 +279,50 @@ def _att_programs(n, bm):
     return [(s, h) for s in starts for h in heads]
 
 
+@functools.lru_cache(maxsize=2)
+def _attention_fp32(name):
+    """softmax(q k^T / sqrt(d)) v of the whole workload in float32 on the GPU, computed per
+    (batch, group of 8 heads) to bound memory: the reference every output element of the
+    timed kernels is compared with. fp32 matmuls on contiguous operands only."""
+    import torch
+    b = _bufs(name)
+    q, k, v = (b[x] for x in "qkv")
+    z, h, n, d = q.shape
+    causal = name == "attention_causal"
+    out = torch.empty((z, h, n, d), dtype=torch.float32, device=q.device)
+    keep = torch.ones(n, n, dtype=torch.bool, device=q.device).tril() if causal else None
+    for zi in range(z):
+        for h0 in range(0, h, 8):
+            qf = q[zi, h0:h0 + 8].float().contiguous()
+            kt = k[zi, h0:h0 + 8].float().transpose(1, 2).contiguous()
+            vf = v[zi, h0:h0 + 8].float().contiguous()
+            sc = torch.matmul(qf, kt) * (d ** -0.5)
+            if causal:
+                sc = sc.masked_fill(~keep, float("-inf"))
+            out[zi, h0:h0 + 8] = torch.matmul(torch.softmax(sc, dim=-1), vf)
+    torch.cuda.synchronize()
+    return out
+
+
 @pytest.mark.parametrize("name,v", [pytest.param(nm, v, id=f"{nm}-" + _id(v))
                                     for nm in ("attention_causal", "attention_noncausal")
                                     for v in TABLE[nm].variants])
 def test_attention_full(name, v):
+    """Every output element of every timed variant against an fp32 reference computed on
+    the GPU (atol 1e-2, rtol 1.6e-2: the bf16 tolerance), plus the oracle and the float64
+    closed form on a stratified sample of programs."""
     import torch
     c = dict(v.constexprs)
     causal = c["CAUSAL"]
     _say(f"{name} bf16 {TABLE[name].describe} {v.label}")
     b, _ = _run(name, v)
+    ref = _attention_fp32(name)
+    err = (b["o"].float() - ref).abs()
+    bound = 1e-2 + 1.6e-2 * ref.abs()
+    bad = int((err > bound).sum())
+    assert bad == 0, f"{bad} of {ref.numel()} output elements outside atol 1e-2 rtol 1.6e-2 " \
+                     f"(max abs error {float(err.max()):.3g})"
+    assert bool(torch.isfinite(b["o"].float()).all())
     got = b["o"].float().cpu().numpy()
     h = _host(name)
     n = h["q"].shape[2]
