@@ -1733,7 +1733,10 @@ class Emitter:
             # workgroups per CU is fastest: the loop is bound by loads in flight, and extra
             # copies cost occupancy and flush work.
             words = sum(i["bins"] for i in self.priv.values())
-            wgs = int(self.opt.get("priv_wgs", 8))
+            # 32 waves per CU (8 per SIMD) at most: an 8-wave program gets 4 workgroups
+            # per CU, all resident at once, rather than 8 of which half would wait for
+            # the first half to finish its walk
+            wgs = int(self.opt.get("priv_wgs", max(1, min(8, 32 // self.nw))))
             cop = int(self.opt.get("priv_copies", 1))
             self.priv_copies = cop
             self.coarsen = 0 if self.opt.get("no_coarsen") else wgs
