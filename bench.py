@@ -182,10 +182,18 @@ def measure(torch, timer, wl, steps, warmup, pin=None):
         ms = timer.run(launches, k, max(2, warmup // 2))
         log(f"    {v.label}: {ms * 1e3:.1f} us")
         if best is None or ms < best[0]:
-            best = (ms, v, launches[0].ck.name, launches[0].shapes)
-    ms, v, kname, shapes = best
+            best = (ms, v, launches[0].ck, launches[0].shapes, launches)
+    ms, v, ck, shapes, launches = best
+    # The same launches one at a time with the GPU idle between them (HIP events around
+    # each, the median of 20): how the library's do_bench and the autotuner sample. The
+    # MFMA rows run faster this way than back to back, where they hold the clock down.
+    from enceladus_amd import testing
+    ms_iso = testing.do_bench(launches[0], warmup_ms=0.0, rep=20)
+    # LDS bytes and registers tell the reported variant's dispatches apart from other
+    # variants of the same grid in a kernel trace
     r.update({"config": f"{wl.describe} {v.label}", "variant": v.label, "ms": ms,
-              "kernel": kname, "dispatches": shapes})
+              "ms_isolated": ms_iso, "kernel": ck.name, "dispatches": shapes, "lds_bytes": ck.attrs["shared_bytes"],
+              "vgprs": ck.attrs["num_regs"]})
     if wl.bound == "hbm":
         r["bytes"] = wl.work
         r["gbps"] = wl.work / ms / 1e6
@@ -492,6 +500,286 @@ def cpu_workload(wl, host, v, budget_s=1.5):
     return out
 
 
+# ------------------------------------------------------------------ profile summaries
+# `python bench.py --summarize-profiles DIR` tabulates the rocprofv3 output of the passes
+# below (run on the GPU box from the repository root, each writing under DIR) into
+# profiles/*.txt. Every summary records the source stamp of the tree the passes measured
+# (from the trace pass's bench JSON), and the bench reads traffic from a summary only while
+# that stamp is the current tree's.
+
+PROFILE_ROWS = ("vector_add,softmax,rmsnorm,matmul,matmul_gelu,attention_causal,"
+                "attention_noncausal,histogram,cumsum,copy_rows,copy_flat,read_flat,fill_flat,"
+                "copy_calib,torch_matmul,torch_sdpa_causal,torch_sdpa_noncausal")
+SQ_COUNTERS = ("SQ_BUSY_CYCLES SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA SQ_INSTS_VALU "
+               "SQ_INSTS_LDS SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE SQ_VALU_MFMA_COEXEC_CYCLES")
+_KERNELS = {"vector_add": ["ek_add_kernel"], "softmax": ["ek_softmax_kernel"],
+            "rmsnorm": ["ek_rmsnorm_kernel"], "matmul": ["ek_matmul_desc_kernel"],
+            "matmul_gelu": ["ek_matmul_bias_gelu_kernel"],
+            "attention_causal": ["ek_attention_kernel"],
+            "attention_noncausal": ["ek_attention_kernel"],
+            "histogram": ["ek_histogram_kernel", "ek_histogram_kernel_flush"],
+            "cumsum": ["ek_cumsum_kernel"], "copy_rows": ["ek_copy_rows_kernel"],
+            "copy_flat": ["ek_copy_flat_kernel"], "read_flat": ["ek_read_flat_kernel"],
+            "fill_flat": ["ek_fill_flat_kernel"]}
+
+
+def profile_commands(pins: str) -> list[str]:
+    """The rocprofv3 passes the summaries come from, as run on the GPU box after
+    `R=<repository root>; D=$R/gpurun_out/prof; cd /tmp && export TMPDIR=/tmp`; the pins
+    come from `python3 $R/bench.py --print-pins $D/trace_bench.json`."""
+    return [
+        "rocprofv3 --kernel-trace --stats -d $D/trace -o run --output-format csv -- "
+        f"python3 $R/bench.py --only {PROFILE_ROWS} --no-cpu-baseline > $D/trace_bench.json",
+        "rocprofv3 --pmc FETCH_SIZE -d $D/FETCH_SIZE -o run --output-format csv -- "
+        f"python3 $R/bench.py --only {PROFILE_ROWS} --pin {pins} --steps 4 --warmup 1 "
+        "--no-cpu-baseline > $D/FETCH_SIZE_bench.json",
+        "rocprofv3 --pmc WRITE_SIZE -d $D/WRITE_SIZE (the same bench.py arguments) > "
+        "$D/WRITE_SIZE_bench.json",
+        f"rocprofv3 --pmc {SQ_COUNTERS} -d $D/sq -o run --output-format csv -- python3 "
+        "$R/bench.py --only matmul,matmul_gelu,attention_causal,attention_noncausal "
+        f"--pin {pins} --steps 3 --warmup 1 --no-cpu-baseline > $D/sq_bench.json"]
+
+
+def profile_pins(trace_json: dict) -> str:
+    """--pin arguments fixing each row to the variant the trace pass's bench reported."""
+    from examples import workloads as W
+    table = W.table()
+    out = []
+    for n, r in trace_json["workloads"].items():
+        if n in table and "variant" in r:
+            labels = [v.label for v in table[n].variants]
+            out.append(f"{n}={labels.index(r['variant'])}")
+    return ",".join(out)
+
+
+def _bench_json(path):
+    return json.loads([ln for ln in open(path) if ln.startswith("{")][-1])
+
+
+def _row_of(kname, grid, block):
+    """The bench row a dispatch of ours belongs to (the two attention configs share a
+    kernel: causal grids have 4096 / BLOCK_M programs on x, non-causal 1024 / BLOCK_M)."""
+    if kname == "ek_attention_kernel":
+        bm = {512: 256, 256: 128, 128: 64}.get(block)
+        if bm is None:
+            return None
+        return {4096: "attention_causal", 1024: "attention_noncausal"}.get(grid[0] * bm)
+    for w, ks in _KERNELS.items():
+        if kname in ks:
+            return w
+    return None
+
+
+def summarize_profiles(d: str) -> None:
+    import collections
+    import csv
+    import statistics
+    import subprocess
+    tj = _bench_json(f"{d}/trace_bench.json")
+    stamp = tj.get("source_stamp")
+    if stamp != source_stamp():
+        raise SystemExit(f"the profiles measured sources {stamp}, this tree is "
+                         f"{source_stamp()}: profile this tree again")
+    try:
+        commit = subprocess.run(["git", "-C", ROOT, "rev-parse", "--short=12", "HEAD"],
+                                capture_output=True, text=True, check=True).stdout.strip()
+        dirty = subprocess.run(["git", "-C", ROOT, "status", "--porcelain", "--",
+                                "enceladus_amd", "examples"], capture_output=True,
+                               text=True).stdout.strip()
+        commit += " (with uncommitted changes)" if dirty else ""
+    except (OSError, subprocess.CalledProcessError):
+        commit = "unknown"
+    pins = profile_pins(tj)
+    cmds = profile_commands(pins)
+    head = ["MI355X (gfx950, 256 CUs), one GPU, ROCm 7.2 rocprofv3; numbers from one gpurun box",
+            f"source_stamp: {stamp}",
+            f"commit: {commit}",
+            "(bench.py --print-stamp gives a tree's stamp; bench.py reports traffic from this "
+            "file only while the stamps agree)", ""]
+    W_ = tj["workloads"]
+    m = statistics.median
+
+    # -- kernel trace -------------------------------------------------------------------
+    rows = list(csv.DictReader(open(f"{d}/trace/run_kernel_trace.csv")))
+    groups, vendor = collections.defaultdict(list), collections.defaultdict(list)
+    for r in rows:
+        name = r["Kernel_Name"]
+        blk = int(r["Workgroup_Size_X"]) * int(r["Workgroup_Size_Y"]) * \
+            int(r["Workgroup_Size_Z"])
+        grid = tuple(int(r[f"Grid_Size_{a}"]) // int(r[f"Workgroup_Size_{a}"]) for a in "XYZ")
+        dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        key = (name, grid, blk, int(r["LDS_Block_Size"]), int(r["VGPR_Count"]),
+               int(r["Accum_VGPR_Count"]))
+        w = _row_of(name, grid, blk)
+        if w is not None:
+            groups[(w,) + key].append(dur)
+        elif name.startswith("Cijk_") or name == "attn_fwd":
+            vendor[key].append(dur)
+    out = ["rocprofv3 kernel trace of every bench.py workload (BASELINE configs, the copy, "
+           "read and write ceilings) and the vendor libraries"] + head + [
+        "command (on the GPU box; R = repository root, D = $R/gpurun_out/prof, run in /tmp "
+        "with TMPDIR=/tmp):",
+        "  " + cmds[0],
+        "tabulated with: python bench.py --summarize-profiles gpurun_out/prof", "",
+        "Per workload: the bench's HIP-event time, then the per-dispatch durations from",
+        "run_kernel_trace.csv grouped by (kernel, grid in workgroups, workgroup size, LDS,",
+        "registers). '*' marks the dispatches of the variant the bench reports, told apart from",
+        "other variants of the same grid by its LDS bytes and registers (a privatised histogram",
+        "launch is two dispatches: the kernel and its _flush); the other rows are the variants",
+        "the bench swept or the autotuner timed. Trace averages include the warm-up, tuning and",
+        "sweep dispatches of the same shape.", ""]
+    hdr = (f"    {'kernel':<30} {'grid (workgroups)':>18} {'wg':>5} {'LDS(B)':>7} {'VGPR':>4} "
+           f"{'AGPR':>4} {'calls':>6} {'avg_us':>8} {'min_us':>8} {'max_us':>8}")
+    for w in _KERNELS:
+        if w not in W_:
+            continue
+        r = W_[w]
+        rep = {(tuple(g), b) for g, b in r["dispatches"]}
+        out += [f"{w}: {r['config']}  ({r['selected_by']})",
+                f"  bench.py HIP events: {r['ms'] * 1e3:.1f} us per launch", hdr]
+        items = sorted(((k, v) for k, v in groups.items() if k[0] == w),
+                       key=lambda kv: -len(kv[1]))
+
+        def reported(k):
+            _, name, grid, blk, lds, vg, _ag = k
+            if (grid, blk) not in rep:
+                return False
+            if name != r["kernel"]:
+                return True                     # the histogram's flush dispatch
+            # the trace rounds LDS up to 512-byte granules and counts registers in pairs
+            return r["lds_bytes"] <= lds < r["lds_bytes"] + 512 and \
+                abs(2 * vg - r["vgprs"]) < 16
+        items.sort(key=lambda kv: not reported(kv[0]))
+        for k, v in items:
+            _, name, grid, blk, lds, vg, ag = k
+            g = "x".join(str(x) for x in grid)
+            out.append(f"  {'*' if reported(k) else ' '} {name:<30} {g:>18} {blk:>5} {lds:>7} "
+                       f"{vg:>4} {ag:>4} {len(v):>6} {statistics.fmean(v):>8.2f} "
+                       f"{min(v):>8.2f} {max(v):>8.2f}")
+        out.append("")
+    out.append("vendor libraries on the same inputs (bench.py torch_* rows):")
+    for t in TORCH_ROWS:
+        if t in W_:
+            out.append(f"  {t}: {W_[t]['config']}: {W_[t]['ms'] * 1e3:.1f} us, "
+                       f"{W_[t]['tflops']:.1f} TFLOP/s")
+    out.append(hdr)
+    for k, v in sorted(vendor.items(), key=lambda kv: kv[0][0]):
+        name, grid, blk, lds, vg, ag = k
+        nm = "Cijk_... (hipBLASLt)" if name.startswith("Cijk_") else "attn_fwd (torch SDPA)"
+        g = "x".join(str(x) for x in grid)
+        out.append(f"    {nm:<30} {g:>18} {blk:>5} {lds:>7} {vg:>4} {ag:>4} {len(v):>6} "
+                   f"{statistics.fmean(v):>8.2f} {min(v):>8.2f} {max(v):>8.2f}")
+    open(os.path.join(ROOT, "profiles", "workloads_kernel_trace.txt"), "w").write(
+        "\n".join(out) + "\n")
+
+    # -- HBM counters -------------------------------------------------------------------
+    def counters(name):
+        per, calib = collections.defaultdict(list), []
+        for r in csv.DictReader(open(f"{d}/{name}/run_counter_collection.csv")):
+            v = float(r["Counter_Value"])
+            if r["Kernel_Name"] == "__amd_rocclr_copyBuffer" and int(r["Grid_Size"]) == 131072:
+                calib.append(v)
+                continue
+            per[(r["Kernel_Name"], int(r["Grid_Size"]), int(r["Workgroup_Size"]))].append(v)
+        return per, calib
+    fetch, fcal = counters("FETCH_SIZE")
+    write, wcal = counters("WRITE_SIZE")
+    jf = _bench_json(f"{d}/FETCH_SIZE_bench.json")["workloads"]
+    ff, wf = 262144 / m(fcal), 262144 / m(wcal)
+    out = ["rocprofv3 HBM counters (FETCH_SIZE, WRITE_SIZE) of every bench.py workload"] + \
+        head + [
+        "commands (on the GPU box, as for the kernel trace), one counter per run, each workload",
+        "pinned to the variant the trace pass's bench reported:",
+        "  " + cmds[1], "  " + cmds[2],
+        "tabulated with: python bench.py --summarize-profiles gpurun_out/prof", "",
+        "calibration (copy_calib: a 256 MiB torch device copy, 262144 KiB read and 262144 KiB "
+        "written):",
+        f"  FETCH_SIZE per dispatch: {m(fcal):.0f} KiB -> factor {ff:.3f}",
+        f"  WRITE_SIZE per dispatch: {m(wcal):.0f} KiB -> factor {wf:.3f}", "",
+        "FETCH_SIZE counts the L2's fetches from memory (HBM, or the Infinity Cache behind the",
+        "L2), so for the MFMA kernels it is L2-miss traffic, an upper bound on HBM bytes.",
+        "Mean per dispatch:", ""]
+    traffic = {}
+    for w in _KERNELS:
+        if w not in jf:
+            continue
+        r = jf[w]
+        out.append(f"{w}: {r['config']}")
+        rd = wr = 0.0
+        for (gx, gy, gz), b in r["dispatches"]:
+            for kname in _KERNELS[w]:
+                k = (kname, gx * gy * gz * b, b)
+                if k in fetch:
+                    fv, wv = statistics.fmean(fetch[k]), statistics.fmean(write[k])
+                    out.append(f"  {kname} ({gx * gy * gz} workgroups x {b}): FETCH_SIZE "
+                               f"{fv:.0f} KiB, WRITE_SIZE {wv:.0f} KiB")
+                    rd += fv * ff
+                    wr += wv * wf
+        tot = round((rd + wr) * 1024)
+        traffic[w] = tot
+        if r["bound"] == "hbm":
+            alg, what = r["bytes"], "algorithmic bytes (the bench's byte count)"
+        elif w.startswith("matmul"):
+            alg = 3 * 4096 * 4096 * 2 + (4096 * 2 if w == "matmul_gelu" else 0)
+            what = "A + B read once, C written once (fp16)"
+        else:
+            n = 4096 if w == "attention_causal" else 1024
+            alg = 4 * 4 * 32 * n * 128 * 2
+            what = "Q, K, V read once, O written once (bf16)"
+        out.append(f"  read {rd:.0f} KiB + written {wr:.0f} KiB = {tot} B per launch; {what}: "
+                   f"{alg} B; measured / algorithmic {tot / alg:.4f}")
+    out += ["", "bench.py reads the lines below into each workload's \"traffic\" (and the "
+            "headline's roofline.traffic):"]
+    out += [f"traffic_bytes_per_launch[{w}]: {t}" for w, t in traffic.items()]
+    open(os.path.join(ROOT, "profiles", "workloads_hbm_counters.txt"), "w").write(
+        "\n".join(out) + "\n")
+
+    # -- SQ counters of the MFMA rows ----------------------------------------------------
+    disp = collections.defaultdict(dict)
+    for r in csv.DictReader(open(f"{d}/sq/run_counter_collection.csv")):
+        e = disp[r["Dispatch_Id"]]
+        e.update(name=r["Kernel_Name"], thr=int(r["Grid_Size"]), wg=int(r["Workgroup_Size"]),
+                 dur=int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+        e[r["Counter_Name"]] = float(r["Counter_Value"])
+    js = _bench_json(f"{d}/sq_bench.json")["workloads"]
+    out = ["rocprofv3 SQ counters of the MFMA workloads (the variants the bench reports)"] + \
+        head + ["command (on the GPU box, as for the kernel trace):",
+                "  " + cmds[3],
+                "tabulated with: python bench.py --summarize-profiles gpurun_out/prof", "",
+                "Counters are summed over the chip; per SIMD = / 1024 (256 CUs x 4 SIMDs). One",
+                "v_mfma_f32_32x32x16 is 32768 FLOP and occupies its SIMD's MFMA unit for 32",
+                "cycles. No clock is derived from these counters: the counters' window is longer",
+                "than the dispatch (a GRBM_GUI_ACTIVE-based clock read above the 2.4 GHz maximum",
+                "on short dispatches). 'MFMA busy at 2.4 GHz' is the MFMA cycles per SIMD over",
+                "the dispatch's duration times the maximum clock: a lower bound on the busy",
+                "fraction, exact only if the kernel ran at 2.4 GHz.", ""]
+    for w in ("matmul", "matmul_gelu", "attention_causal", "attention_noncausal"):
+        if w not in js:
+            continue
+        r = js[w]
+        ((gx, gy, gz), b), = r["dispatches"]
+        ds = [e for e in disp.values() if e["name"] == r["kernel"] and
+              e["thr"] == gx * gy * gz * b and e["wg"] == b and "SQ_INSTS_MFMA" in e]
+        mf = m([e["SQ_INSTS_MFMA"] for e in ds])
+        va = m([e["SQ_INSTS_VALU"] for e in ds])
+        busy = m([e["SQ_VALU_MFMA_BUSY_CYCLES"] for e in ds]) / 1024
+        co = m([e["SQ_VALU_MFMA_COEXEC_CYCLES"] for e in ds]) / 1024
+        lds = m([e["SQ_INSTS_LDS"] for e in ds])
+        bc = m([e["SQ_LDS_BANK_CONFLICT"] for e in ds])
+        dur = m([e["dur"] for e in ds])
+        out += [f"{w}: {r['config']}",
+                f"  {len(ds)} dispatches, median duration {dur / 1e3:.1f} us",
+                f"  MFMA busy per SIMD {busy:.0f} cycles = {100 * busy / (dur * 2.4):.1f}% of the "
+                f"dispatch at 2.4 GHz; MFMA/VALU co-issue {co:.0f} cycles per SIMD",
+                f"  SQ_INSTS_MFMA {mf:.0f} (x 32768 FLOP = {mf * 32768 / r['flop']:.4f} x the "
+                f"algorithmic FLOP), SQ_INSTS_VALU {va:.0f} ({va / mf:.2f} per MFMA)",
+                f"  SQ_INSTS_LDS {lds:.0f}, SQ_LDS_BANK_CONFLICT {bc:.0f} "
+                f"({bc / lds:.3f} per LDS instruction)", ""]
+    open(os.path.join(ROOT, "profiles", "matmul_attention_sq_counters.txt"), "w").write(
+        "\n".join(out) + "\n")
+    print(f"wrote profiles/ from {d} (source_stamp {stamp}, commit {commit}, pins {pins})")
+
+
 # ----------------------------------------------------------------------------- main
 
 def main():
@@ -506,9 +794,19 @@ def main():
                     "variant of the workload's table (profiling runs)")
     ap.add_argument("--print-stamp", action="store_true", help="print the source stamp "
                     "that counter summaries record, and exit")
+    ap.add_argument("--print-pins", metavar="BENCH_JSON", help="print the --pin arguments "
+                    "that fix every row to the variant a bench run reported, and exit")
+    ap.add_argument("--summarize-profiles", metavar="DIR", help="tabulate the rocprofv3 "
+                    "passes under DIR into profiles/*.txt, and exit (no GPU needed)")
     args = ap.parse_args()
     if args.print_stamp:
         print(source_stamp())
+        return
+    if args.print_pins:
+        print(profile_pins(_bench_json(args.print_pins)))
+        return
+    if args.summarize_profiles:
+        summarize_profiles(args.summarize_profiles)
         return
     pins = {k: int(v) for k, v in (p.split("=") for p in args.pin.split(",") if p)}
     if args.gpus != 1:
@@ -548,7 +846,8 @@ def main():
         results[n] = r
         log(f"[bench] {n}: {r['ms'] * 1e3:.1f} us  " +
             (f"{r['gbps']:.0f} GB/s" if "gbps" in r else f"{r['tflops']:.1f} TFLOP/s") +
-            f"  ({100 * r['roofline_frac']:.1f}% of roofline)")
+            f"  ({100 * r['roofline_frac']:.1f}% of roofline; isolated launches "
+            f"{r['ms_isolated'] * 1e3:.1f} us)")
         if not args.no_cpu_baseline and not table[n].ceiling:
             v = next(x for x in table[n].variants if x.label == r["variant"])
             cpu[n] = cpu_workload(table[n], host, v)

@@ -122,8 +122,10 @@ int ek_timed_launch(void* stream, void* function, uint32_t gx, uint32_t gy, uint
  * them. Block sizes are 1-D. Fails, launching nothing, when `scratch_bytes` exceeds
  * EK_SCRATCH_BYTES. Calls no allocating routine. Every call on one GPU shares that GPU's
  * array: calls that overlap on one GPU (other streams, other threads) race; calls in one
- * stream's order do not. The kernels write every partial word they read, so nothing needs
- * clearing between calls. */
+ * stream's order do not. Nothing needs clearing between calls: the first kernel writes
+ * every bin word of the partial rows before the flush kernel reads it. The flush's 16-byte
+ * loads also read the padding words between bin groups (bin counts are rounded up to 4),
+ * which no kernel writes; no atomic targets them, so their stale contents are discarded. */
 #define EK_SCRATCH_BYTES (16u << 20)
 int ek_launch_flush_noalloc(void* stream, void* function, uint32_t gx, uint32_t gy,
                             uint32_t gz, uint32_t block, const void* kernarg,
