@@ -120,6 +120,11 @@ class CompiledKernel:
 
     def function(self):
         if self._function is None:
+            if "ek::mfma_" in self.hip or "ek::Gemm" in self.hip:
+                # before the first MFMA kernel of the process runs: the device's MFMA lane
+                # maps are the ones the emitter assumes (reference: compile.py:159-160)
+                from enceladus_amd.runtime.probe import check_mfma_layout
+                check_mfma_layout()
             m = ctypes.c_void_p()
             buf = ctypes.create_string_buffer(self.code, len(self.code))
             hip.call("ek_module_load", buf, len(self.code), ctypes.byref(m))
