@@ -40,3 +40,23 @@ def test_explain_names_the_mfma_plan_of_each_dot():
     dots = [ln for ln in text.splitlines() if "(MxNxK)" in ln]
     assert len(dots) == 2 and all("wave grid 8x1" in d and "MFMA 32x32x16" in d for d in dots)
     assert all("staged through LDS" in d for d in dots)
+
+
+def test_explain_on_a_cache_hit_reports_the_kernel_that_was_loaded(monkeypatch, tmp_path):
+    """A specialization loaded from the persistent cache has no emitter report; explain
+    regenerates it with the options the kernel was compiled with (the ENCELADUS_CODEGEN
+    switches included), so it describes the loaded kernel."""
+    from enceladus_amd.runtime.jit import JITFunction
+    from examples.matmul import matmul_desc_kernel
+    monkeypatch.setenv("ENCELADUS_CACHE_DIR", str(tmp_path))
+    monkeypatch.setenv("ENCELADUS_CODEGEN", "no_gemm_template")
+    a = np.zeros((256, 256), np.float16)
+    args = (a, a, a, 256, 256, 256, 256, 256, 256)
+    kw = dict(BM=128, BN=128, BK=64, num_warps=4)
+    first = JITFunction(matmul_desc_kernel.fn).warmup(*args, **kw)
+    assert first.gen.report is not None and "GemmDma" not in first.hip
+    fresh = JITFunction(matmul_desc_kernel.fn)          # empty in-memory cache: a disk hit
+    ck = fresh.warmup(*args, **kw)
+    assert ck.gen.report is None and ck.hip == first.hip
+    text = fresh.explain(*args, **kw)
+    assert "GEMM template" not in text and "MFMA 32x32x16" in text
