@@ -126,7 +126,7 @@ def test_missing_tl_name_is_a_compilation_error():
 
 SUBMODULES = [
     "compiler", "compiler.errors", "compiler.ir", "compiler.frontend", "compiler.semantic",
-    "compiler.layout", "compiler.explain", "runtime", "runtime.autotuner", "runtime.jit",
+    "compiler.layout", "compiler.explain", "compiler.pipeline", "runtime", "runtime.autotuner", "runtime.jit",
     "runtime.device", "runtime.tensor", "runtime.debug", "runtime.raw", "language",
     "language.core", "language.ops", "language.math", "configs", "testing",
 ]
@@ -238,3 +238,19 @@ def test_warm_key_refuses_extra_positional_arguments():
     assert k._make_binder(3, (), (3, 4, 5), {})((3, 4, 5), {}, 4, None) is None
     with pytest.raises(TypeError):
         k.bind((3, 4, 5), {})
+
+
+def test_compile_module_at_the_reference_path():
+    """reference tests/test_codegen.py:85-87 compile a kernel's IR through
+    `enceladus.compiler.pipeline.compile_module` and compare sources."""
+    import numpy as np
+
+    from enceladus.compiler.pipeline import compile_module
+    from tests.test_explain import _transposed_sum
+    a = np.zeros((64, 64), np.float32)
+    out = np.zeros(64, np.float32)
+    first = compile_module(_transposed_sum.ir(a, a, out, N=64))
+    second = compile_module(_transposed_sum.ir(a, a, out, N=64))
+    assert first.source == second.source and "ek__transposed_sum" in first.source
+    with pytest.raises(Exception, match="LDS"):
+        compile_module(_transposed_sum.ir(a, a, out, N=64), max_threadgroup_memory=16)
