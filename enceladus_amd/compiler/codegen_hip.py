@@ -2400,6 +2400,18 @@ class Emitter:
             self.emit("#pragma unroll")
             self.emit(f"for (int r = 0; r < {lc.nregs}; ++r) {nm}[r] = ek::f32({e});")
         tm, tn, tk, kpl = plan.tm, plan.tn, plan.tk, ins.kpl
+        sp = getattr(self, "split_next", None)
+        if sp is not None and sp["scope"] is self.cur and \
+                any(x is not None and x[0] is sp["info"] for x in (sa, sb)):
+            # split stages: every wave is done reading the first dot's stage and this wave's
+            # copies of this dot's operand have landed; after the barrier everyone's have,
+            # and the first dot's operand for the next iteration can be copied under this dot
+            self.emit('asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\\n\\ts_barrier" ::: '
+                      '"memory");')
+            su, ch = sp["parts"]
+            self.deferred_dma = {"lines": ["{"] + ["  " + ln for ln in su + ch] + ["}"],
+                                 "setup": su, "chunks": ch, "used": False, "scope": self.cur}
+            self.split_next = None
         dd = getattr(self, "deferred_dma", None)
         copies = {}
         if (sa or sb) and dd is not None and not dd["used"] and tk > 1 and \
@@ -2704,6 +2716,42 @@ class Emitter:
         sl = best[1]
         _STAGE_LAYOUTS[key] = (sl, best[0][0], LDS.ideal(acc))
         return sl
+
+    def _split_stages(self, stg: list, body, per_stage: int):
+        """(first, second) stage infos when a loop's two staged operands are better served
+        by one LDS stage each than by two: each operand feeds its own `tl.dot` at the top
+        level of the body, one dot after the other (attention's QK^T, then PV); the
+        workgroup has at most 4 waves; and double-buffered stages would take more than half
+        of the CU's LDS while single ones fit in half, so two workgroups can share a CU.
+        The second operand is then copied under the first dot and the first operand's next
+        tile under the second dot, with a barrier between the dots, and the other
+        workgroup on the CU covers each one's waits (a 128x128 attention tile, causal:
+        547 against 750 us with two stages each, and against 568 us for 256x128 with 8
+        waves). None otherwise, or with ENCELADUS_CODEGEN=no_split_stages."""
+        if self.opt.get("no_split_stages") or len(stg) != 2 or self.nt > 256 or \
+                not (per_stage <= 81920 < 2 * per_stage):
+            return None
+        ids = {info["op"].result.id: info for info in stg}
+        order = []
+        for o in body.ops:
+            if o.name != "dot":
+                continue
+            hit = [ids[_through_trans(x).id] for x in o.operands[:2]
+                   if _through_trans(x).id in ids]
+            if len(hit) > 1:
+                return None
+            if hit:
+                plan = self.dot_plans.get(o.result.id)
+                if plan is None or plan.tk < 2 or hit[0] in order:
+                    return None
+                order.append(hit[0])
+        if len(order) != 2:
+            return None
+        for info in stg:
+            for u in self.uses.get(info["op"].result.id, []):
+                if u.name not in ("dot", "trans"):
+                    return None
+        return order[0], order[1]
 
     def _stage_dma_parts(self, info, kval: str, stage: str) -> tuple[list[str], list[str]]:
         """Copies the tile at row origin `kval` (or the loop-invariant one) into stage `stage`,
@@ -3102,6 +3150,9 @@ class Emitter:
             dcount = sum(info["R"] * info["C"] // 8 // self.nt for info in stg)
             while nst > 2 and (nst - 2) * dcount > 63:
                 nst -= 1
+            split = self._split_stages(stg, body, per_stage)
+            if split is not None:
+                nst = 1
             for info in stg:
                 info["loop_idx"] = li
                 self._stage_setup_dma(info, len(self.extra_smem), nst)
@@ -3109,6 +3160,10 @@ class Emitter:
             # nothing loaded before the loop is outstanding, so the vmcnt at the top of the
             # body counts this loop's copies only
             self.emit("__builtin_amdgcn_s_waitcnt(0x0F70);")
+            if split is not None:
+                # split stages: only the first dot's operand is copied ahead of the loop
+                for ln in self._stage_dma(split[0], lo, "0"):
+                    self.emit(ln)
             for s_ in range(nst - 1):
                 for info in stg:
                     kv = f"({lo} + {s_} * {step})" if s_ else lo
@@ -3142,10 +3197,19 @@ class Emitter:
             # this wave's copies of the current stage have landed (nst - 2 younger stages may
             # still fly) and its reads of the previous stage are complete; after the barrier
             # everyone's are, so the previous stage can be refilled.
-            self.emit(f'asm volatile("s_waitcnt vmcnt({(nst - 2) * dcount}) lgkmcnt(0)\\n\\t'
-                      f's_barrier" ::: "memory");')
+            self.emit(f'asm volatile("s_waitcnt vmcnt({max(0, nst - 2) * dcount}) lgkmcnt(0)'
+                      f'\\n\\ts_barrier" ::: "memory");')
             setup, chunks = [], []
-            for info in stg:
+            if split is not None:
+                # split stages: the second dot's operand for this iteration is copied under
+                # the first dot; the first dot's operand for the next iteration is copied
+                # under the second dot, after a barrier between them (`op_dot`)
+                setup, chunks = self._stage_dma_parts(split[1], ivn, "0")
+                prev_split = getattr(self, "split_next", None)
+                self.split_next = {"info": split[1], "scope": self.cur,
+                                   "parts": self._stage_dma_parts(split[0],
+                                                                  f"({ivn} + {step})", "0")}
+            for info in (stg if split is None else ()):
                 su, ch = self._stage_dma_parts(info, f"({ivn} + {nst - 1} * {step})",
                                                f"(ek_it{li} + {nst - 1}) % {nst}")
                 setup += su
@@ -3176,6 +3240,9 @@ class Emitter:
             if d is not None and not d["used"]:
                 slot.extend(self.cur.indent + ln for ln in d["lines"])
             self.deferred_dma = prev_dma
+            if split is not None:
+                assert self.split_next is None, "split stages: the second dot never ran"
+                self.split_next = prev_split
             self.emit(f"++ek_it{li};")
             self.in_staged_loop -= 1
         elif stg:

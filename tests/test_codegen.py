@@ -416,3 +416,34 @@ def test_program_versioning():
     assert "__builtin_amdgcn_s_waitcnt(0x0F70)" not in serial
     two = codegen_hip.generate(_store_then_load.ir_for(x, x, 1 << 20, BLOCK=1024)).source
     assert "__builtin_expect(" not in two
+
+
+def _attention_source(bm, bn, nw, monkeypatch=None, **env):
+    import torch
+
+    from examples.flash_attention import attention_kernel
+    bf = torch.zeros(16, dtype=torch.bfloat16)
+    ck = attention_kernel.warmup(bf, bf, bf, bf, 0.088, 4096, 4096 * 128, 128, HEAD_DIM=128,
+                                 BLOCK_M=bm, BLOCK_N=bn, CAUSAL=True, num_warps=nw,
+                                 dot_warps=(nw, 1))
+    return ck
+
+
+def test_split_stages_for_a_four_wave_attention_tile(monkeypatch):
+    """128x128 over 4 waves: one LDS stage each for K and V (64 KB, so two workgroups share a
+    CU); V is copied under QK^T, the next K under PV, with a barrier between the dots.
+    256x128 over 8 waves keeps two stages each (registers already limit it to one workgroup
+    per CU), and ENCELADUS_CODEGEN=no_split_stages restores them."""
+    ck = _attention_source(128, 128, 4)
+    src = ck.hip
+    assert ck.lds_bytes == 65536
+    loop = src[src.index("for (int32_t iv"):src.index("++ek_it")]
+    assert loop.count("s_barrier") == 2
+    first, second = loop.split("s_barrier")[1], loop.split("s_barrier")[2]
+    # the V tile of this iteration goes out under the first dot (descriptor a2 = v_ptr),
+    # the K tile of the next iteration under the second (a1 = k_ptr)
+    assert "rsrc_words(s8" in first and "_r0 = iv" in first
+    assert "rsrc_words(s7" in second and "+ s5)" in second
+    assert _attention_source(256, 128, 8).lds_bytes == 131072
+    monkeypatch.setenv("ENCELADUS_CODEGEN", "no_split_stages")
+    assert _attention_source(128, 128, 4).lds_bytes == 131072
