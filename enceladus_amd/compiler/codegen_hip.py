@@ -997,9 +997,24 @@ class Emitter:
         self.def_level[v.id] = len(self.scopes) - 1
 
     # ------------------------------------------------------------------ ops
-    def gen_block(self, block: ir.Block):
-        for op in block.ops:
+    def gen_block(self, block: ir.Block, ops=None):
+        for op in (block.ops if ops is None else ops):
+            sp = getattr(self, "split_next", None)
+            if sp is not None and sp.get("at") is op:
+                self._split_barrier(sp)
             self.gen_op(op)
+
+    def _split_barrier(self, sp):
+        """Split stages: every wave is done reading the first dot's stage and this wave's
+        copies of the second dot's operand have landed; after the barrier everyone's have,
+        and the first dot's operand for the next iteration can be copied under the second
+        dot."""
+        self.emit('asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\\n\\ts_barrier" ::: '
+                  '"memory");')
+        su, ch = sp["parts"]
+        self.deferred_dma = {"lines": ["{"] + ["  " + ln for ln in su + ch] + ["}"],
+                             "setup": su, "chunks": ch, "used": False, "scope": self.cur}
+        self.split_next = None
 
     def gen_op(self, op: ir.Op):
         prev = getattr(self, "cur_op", None)
@@ -2403,15 +2418,7 @@ class Emitter:
         sp = getattr(self, "split_next", None)
         if sp is not None and sp["scope"] is self.cur and \
                 any(x is not None and x[0] is sp["info"] for x in (sa, sb)):
-            # split stages: every wave is done reading the first dot's stage and this wave's
-            # copies of this dot's operand have landed; after the barrier everyone's have,
-            # and the first dot's operand for the next iteration can be copied under this dot
-            self.emit('asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\\n\\ts_barrier" ::: '
-                      '"memory");')
-            su, ch = sp["parts"]
-            self.deferred_dma = {"lines": ["{"] + ["  " + ln for ln in su + ch] + ["}"],
-                                 "setup": su, "chunks": ch, "used": False, "scope": self.cur}
-            self.split_next = None
+            self._split_barrier(sp)
         dd = getattr(self, "deferred_dma", None)
         copies = {}
         if (sa or sb) and dd is not None and not dd["used"] and tk > 1 and \
@@ -2728,11 +2735,12 @@ class Emitter:
         workgroup on the CU covers each one's waits (a 128x128 attention tile, causal:
         547 against 750 us with two stages each, and against 568 us for 256x128 with 8
         waves). None otherwise, or with ENCELADUS_CODEGEN=no_split_stages."""
+        force = self.opt.get("split_stages") == "force"
         if self.opt.get("no_split_stages") or len(stg) != 2 or self.nt > 256 or \
-                not (per_stage <= 81920 < 2 * per_stage):
+                per_stage > 81920 or not (force or 81920 < 2 * per_stage):
             return None
         ids = {info["op"].result.id: info for info in stg}
-        order = []
+        order, dots = [], []
         for o in body.ops:
             if o.name != "dot":
                 continue
@@ -2745,13 +2753,67 @@ class Emitter:
                 if plan is None or plan.tk < 2 or hit[0] in order:
                     return None
                 order.append(hit[0])
+                dots.append(o)
         if len(order) != 2:
             return None
         for info in stg:
             for u in self.uses.get(info["op"].result.id, []):
                 if u.name not in ("dot", "trans"):
                     return None
-        return order[0], order[1]
+        return order[0], order[1], dots[0], dots[1]
+
+    # ops that read nothing but their operands and memory no op in the loop body writes
+    _SINKABLE = frozenset(("binary", "unary", "cast", "select", "fma", "splat", "broadcast",
+                           "expand_dims", "trans", "reshape", "const", "arange", "reduce",
+                           "desc_load", "hint", "bitcast"))
+
+    def _split_sink(self, body, first, second):
+        """The loop body's ops in the order that puts the barrier between the dots of a
+        split-stage loop (see `_split_stages`) as late as it can go: the ops between the two
+        dots that build the second dot's A operand from a row reduction of the first dot's
+        result (attention: `p = exp2(qk * scale - m)` and its cast), and everything that
+        uses them (the row sum of p), move after the others (the row max, the rescale
+        factor, `acc * alpha`), keeping their relative order. Returns (ops, first moved op),
+        the barrier going right before that op, or None when there is nothing to move, an
+        op in between has a region or a side effect, or ENCELADUS_CODEGEN=no_split_sink.
+
+        The moved ops then form one basic block with the second dot's MFMAs (the rescale's
+        skip branch stays before the barrier), which lets the compiler issue the
+        exponentials of key slice k+1 while slice k's MFMAs run (causal 128x128: 3.5%
+        faster than the barrier right before the second dot)."""
+        if self.opt.get("no_split_sink"):
+            return None
+        ops = body.ops
+        i1, i2 = ops.index(first), ops.index(second)
+        between = ops[i1 + 1:i2]
+        if any(o.name not in self._SINKABLE or o.regions for o in between):
+            return None
+        inside = {id(o) for o in between}
+
+        def producers(o):
+            return [x.op for x in o.operands if x.op is not None and id(x.op) in inside]
+
+        a = second.operands[0]
+        anc, todo = set(), [a.op] if a.op is not None and id(a.op) in inside else []
+        while todo:
+            o = todo.pop()
+            if id(o) not in anc:
+                anc.add(id(o))
+                todo.extend(producers(o))
+        after_reduce = set()
+        for o in between:
+            if o.name == "reduce" or any(id(p) in after_reduce for p in producers(o)):
+                after_reduce.add(id(o))
+        moved = {id(o) for o in between if id(o) in anc and id(o) in after_reduce and
+                 o.name != "reduce" and o.results and o.result.type.shape == a.type.shape}
+        if not moved:
+            return None
+        for o in between:
+            if any(id(p) in moved for p in producers(o)):
+                moved.add(id(o))
+        keep = [o for o in between if id(o) not in moved]
+        sunk = [o for o in between if id(o) in moved]
+        return ops[:i1 + 1] + keep + sunk + ops[i2:], sunk[0]
 
     def _stage_dma_parts(self, info, kval: str, stage: str) -> tuple[list[str], list[str]]:
         """Copies the tile at row origin `kval` (or the loop-invariant one) into stage `stage`,
@@ -3192,6 +3254,7 @@ class Emitter:
         self.define(iv, ivn)
         for a, nm in zip(carried, names):
             self.define(a, nm)
+        body_ops = None
         if dma:
             self.in_staged_loop = getattr(self, "in_staged_loop", 0) + 1
             # this wave's copies of the current stage have landed (nst - 2 younger stages may
@@ -3209,6 +3272,9 @@ class Emitter:
                 self.split_next = {"info": split[1], "scope": self.cur,
                                    "parts": self._stage_dma_parts(split[0],
                                                                   f"({ivn} + {step})", "0")}
+                sink = self._split_sink(body, split[2], split[3])
+                if sink is not None:
+                    body_ops, self.split_next["at"] = sink
             for info in (stg if split is None else ()):
                 su, ch = self._stage_dma_parts(info, f"({ivn} + {nst - 1} * {step})",
                                                f"(ek_it{li} + {nst - 1}) % {nst}")
@@ -3234,7 +3300,7 @@ class Emitter:
                 for ln in self._stage_load(info, f"({ivn} + {step})"):
                     self.emit("  " + ln)
             self.emit("}")
-        self.gen_block(body)
+        self.gen_block(body, body_ops)
         if dma:
             d = self.deferred_dma
             if d is not None and not d["used"]:
@@ -3459,7 +3525,7 @@ class Emitter:
         elif self.dot_plans and self.nt <= 256 and not self.opt.get("no_occupancy_hint"):
             # Two waves per SIMD for MFMA loops: the second wave covers LDS and barrier
             # latency. hiprtc otherwise settles on one wave when it can use >256 registers.
-            attrs += " __attribute__((amdgpu_waves_per_eu(2)))"
+            attrs += f" __attribute__((amdgpu_waves_per_eu({int(self.opt.get('waves_per_eu', 2))})))"
         out.append(f'extern "C" __global__ void {attrs} {kname}('
                    + ", ".join(params) + ") {")
         # Stage buffers share the LDS block with the scratch used for conversions and

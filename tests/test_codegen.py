@@ -444,6 +444,19 @@ def test_split_stages_for_a_four_wave_attention_tile(monkeypatch):
     # the K tile of the next iteration under the second (a1 = k_ptr)
     assert "rsrc_words(s8" in first and "_r0 = iv" in first
     assert "rsrc_words(s7" in second and "+ s5)" in second
+    # the barrier between the dots sits after the row max and the rescale of the
+    # accumulator (its skip branch is the ballot) and before the exponentials of the scores,
+    # their row sum and their cast, which share one basic block with PV's MFMAs
+    ex = "ek::exp2_fast(__builtin_fmaf("
+    assert "ek::Max::op" in first and "__builtin_amdgcn_ballot_w64" in first
+    assert ex not in first and ex in second
+    assert second.index(ex) < second.index("ek::Sum::op") < second.index("ek::cvt<ek::bf16>") \
+        < second.index("ek::mfma_32x32x16")
+    monkeypatch.setenv("ENCELADUS_CODEGEN", "no_split_sink")
+    late = _attention_source(128, 128, 4).hip
+    late = late[late.index("for (int32_t iv"):late.index("++ek_it")].split("s_barrier")
+    assert ex in late[1] and "ek::cvt<ek::bf16>" in late[1]
+    monkeypatch.delenv("ENCELADUS_CODEGEN")
     assert _attention_source(256, 128, 8).lds_bytes == 131072
     monkeypatch.setenv("ENCELADUS_CODEGEN", "no_split_stages")
     assert _attention_source(128, 128, 4).lds_bytes == 131072
