@@ -456,7 +456,9 @@ EK_INLINE void mfma_16x16x32(int32_t* acc, const int8_t* a, const int8_t* b) {
 //
 // NT threads = WM x WN waves; each wave owns a (BM/WM) x (BN/WN) block of 32x32 MFMA tiles
 // (v_mfma_f32_32x32x16_{f16,bf16}). The accumulator is held in the emitter's MFMA layout:
-// acc[(tm * TN + tn) * 16 + j].
+// acc[(tm * TN + tn) * 16 + j]. With TR the instruction computes each tile's transpose
+// (B^T A^T, the same fragments in swapped slots), so a lane holds one row of C and 4
+// consecutive columns per 4 registers instead of one column and 4 rows.
 //
 // Per iteration each thread prefetches its share of the next A and B tiles from global
 // memory into registers (16-byte loads), computes the current tile from LDS, then writes
@@ -625,7 +627,8 @@ EK_INLINE void dma16(i32x4 rsrc, uint32_t lds, int voff) {
                ::"s"(lds), "v"(voff), "s"(rsrc) : "memory", "m0");
 }
 
-template <typename T, int BM, int BN, int BK, int WM, int WN, int NT, bool BUF = false>
+template <typename T, int BM, int BN, int BK, int WM, int WN, int NT, bool BUF = false,
+          bool TR = false>
 struct Gemm {
   static constexpr int TM = BM / WM / 32, TN = BN / WN / 32, TK = BK / 16;
   static constexpr int KC = BK / 8;                    // 16-byte chunks per k row
@@ -757,7 +760,10 @@ struct Gemm {
 #pragma unroll
       for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-        for (int tn = 0; tn < TN; ++tn) mfma_32x32x16(&acc[(tm * TN + tn) * 16], a[tm], b[tn]);
+        for (int tn = 0; tn < TN; ++tn) {
+          if constexpr (TR) mfma_32x32x16(&acc[(tm * TN + tn) * 16], b[tn], a[tm]);
+          else mfma_32x32x16(&acc[(tm * TN + tn) * 16], a[tm], b[tn]);
+        }
     }
   }
 
@@ -808,7 +814,8 @@ struct Gemm {
 //    k * NCB + (nc ^ (((k >> RSH) & RMASK) << 2)), which spreads the 4 rows a transpose
 //    read touches over the 4 64-byte quarters of a pass.
 // ---------------------------------------------------------------------------
-template <typename T, int BM, int BN, int BK, int WM, int WN, int NT, int S, int SPLIT = 1>
+template <typename T, int BM, int BN, int BK, int WM, int WN, int NT, int S, int SPLIT = 1,
+          bool TR = false>
 struct GemmDma {
   static constexpr int TM = BM / WM / 32, TN = BN / WN / 32, TK = BK / 16;
   static constexpr int KC = BK / 8;                       // A chunks per row
@@ -916,7 +923,10 @@ struct GemmDma {
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-      for (int tn = 0; tn < TN; ++tn) mfma_32x32x16(&acc[(tm * TN + tn) * 16], a[tm], b[tn]);
+      for (int tn = 0; tn < TN; ++tn) {
+        if constexpr (TR) mfma_32x32x16(&acc[(tm * TN + tn) * 16], b[tn], a[tm]);
+        else mfma_32x32x16(&acc[(tm * TN + tn) * 16], a[tm], b[tn]);
+      }
   }
 
   template <int KK0, int KK1>

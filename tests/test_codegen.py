@@ -150,12 +150,20 @@ def test_descriptor_dot_loop_uses_gemm_template():
     f16 = np.zeros(16, np.float16)
     src = codegen_hip.generate(matmul_desc_kernel.ir_for(
         f16, f16, f16, 4096, 4096, 4096, 4096, 4096, 4096, BM=256, BN=256, BK=64)).source
-    # aligned operands within 2 GiB: the LDS-DMA pipeline (64 KB stages, 2 of them)
-    assert "ek::GemmDma<_Float16, 256, 256, 64, 2, 2, 256, 2, 1>" in src
+    # aligned operands within 2 GiB: the LDS-DMA pipeline (64 KB stages, 2 of them); the
+    # MFMAs compute C^T, so each lane holds 4 consecutive columns of a row and the epilogue
+    # writes 8-byte runs to LDS
+    assert "ek::GemmDma<_Float16, 256, 256, 64, 2, 2, 256, 2, 1, true>" in src
+    assert "ek::vstore<_Float16, 4>(&sm[" in src
     # K and N not known to be multiples of 8: the template reads the row tails elementwise
     src3 = codegen_hip.generate(matmul_desc_kernel.ir_for(
         f16, f16, f16, 256, 250, 100, 112, 256, 250, BM=128, BN=128, BK=64)).source
-    assert "ek::Gemm<_Float16, 128, 128, 64, 2, 2, 256, false>" in src3
+    assert "ek::Gemm<_Float16, 128, 128, 64, 2, 2, 256, false, true>" in src3
+    # ENCELADUS_CODEGEN=no_acc_transpose: the instruction's own orientation
+    src4 = codegen_hip.generate(matmul_desc_kernel.ir_for(
+        f16, f16, f16, 4096, 4096, 4096, 4096, 4096, 4096, BM=256, BN=256, BK=64),
+        {"no_acc_transpose": True}).source
+    assert "ek::GemmDma<_Float16, 256, 256, 64, 2, 2, 256, 2, 1>" in src4
     # unaligned strides fall back to the generic lowering
     src2 = codegen_hip.generate(matmul_desc_kernel.ir_for(
         f16, f16, f16, 100, 90, 70, 70, 90, 90, BM=64, BN=64, BK=32)).source
