@@ -468,3 +468,51 @@ def test_split_stages_for_a_four_wave_attention_tile(monkeypatch):
     assert _attention_source(256, 128, 8).lds_bytes == 131072
     monkeypatch.setenv("ENCELADUS_CODEGEN", "no_split_stages")
     assert _attention_source(128, 128, 4).lds_bytes == 131072
+
+
+@enceladus.jit
+def _attention_with_row_stats(q_ptr, k_ptr, v_ptr, o_ptr, m_ptr, sm_scale, N_CTX, stride_m,
+                              HEAD_DIM: tl.constexpr, BLOCK_M: tl.constexpr,
+                              BLOCK_N: tl.constexpr):
+    """The attention body with a store of the running row max inside the loop."""
+    start_m = tl.program_id(0)
+    q_desc = tl.make_tensor_descriptor(q_ptr, [N_CTX, HEAD_DIM], [stride_m, 1],
+                                       [BLOCK_M, HEAD_DIM])
+    k_desc = tl.make_tensor_descriptor(k_ptr, [N_CTX, HEAD_DIM], [stride_m, 1],
+                                       [BLOCK_N, HEAD_DIM])
+    v_desc = tl.make_tensor_descriptor(v_ptr, [N_CTX, HEAD_DIM], [stride_m, 1],
+                                       [BLOCK_N, HEAD_DIM])
+    o_desc = tl.make_tensor_descriptor(o_ptr, [N_CTX, HEAD_DIM], [stride_m, 1],
+                                       [BLOCK_M, HEAD_DIM])
+    offs_m = start_m * BLOCK_M + tl.arange(0, BLOCK_M)
+    m_i = tl.full([BLOCK_M], float("-inf"), tl.float32)
+    l_i = tl.zeros([BLOCK_M], tl.float32)
+    acc = tl.zeros([BLOCK_M, HEAD_DIM], tl.float32)
+    q = q_desc.load([start_m * BLOCK_M, 0])
+    for start_n in range(0, N_CTX, BLOCK_N):
+        qk = tl.dot(q, tl.trans(k_desc.load([start_n, 0]))) * sm_scale
+        m_ij = tl.maximum(m_i, tl.max(qk, 1))
+        tl.store(m_ptr + offs_m, m_ij)
+        p = tl.exp2(qk - m_ij[:, None])
+        alpha = tl.exp2(m_i - m_ij)
+        l_i = l_i * alpha + tl.sum(p, 1)
+        acc = acc * alpha[:, None]
+        acc = tl.dot(p.to(q_desc.dtype), v_desc.load([start_n, 0]), acc)
+        m_i = m_ij
+    o_desc.store([start_m * BLOCK_M, 0], (acc / l_i[:, None]).to(o_desc.dtype))
+
+
+def test_split_sink_keeps_source_order_around_a_store():
+    """An op with a side effect between the two dots (here a store of the row max) leaves
+    the split-stage loop in source order: the exponentials stay before the barrier."""
+    import torch
+    bf = torch.zeros(16, dtype=torch.bfloat16)
+    f32 = np.zeros(16, np.float32)
+    src = codegen_hip.generate(_attention_with_row_stats.ir_for(
+        bf, bf, bf, bf, f32, 0.088, 4096, 128, HEAD_DIM=128, BLOCK_M=128, BLOCK_N=128,
+        num_warps=4, dot_warps=(4, 1))).source
+    loop = src[src.index("for (int32_t iv"):src.index("++ek_it")]
+    parts = loop.split("s_barrier")
+    assert len(parts) == 3, "expected the split-stage loop (two barriers)"
+    assert "ek::exp2_fast(__builtin_fmaf(" in parts[1] and "ek::cvt<ek::bf16>" in parts[1]
+    assert "ek::exp2_fast(" not in parts[2]
