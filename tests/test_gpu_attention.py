@@ -31,6 +31,9 @@ CASES = [
     ("float32", 100, 128, True, (32, 32, 1)),
     ("bfloat16", 100, 64, False, (32, 16, 1)),
     ("bfloat16", 300, 128, True, (128, 64, 4)),
+    # one LDS stage each for K and V, the exponentials behind the mid barrier (split stages)
+    ("bfloat16", 300, 128, True, (128, 128, 4)),
+    ("float16", 300, 128, False, (128, 128, 4)),
 ]
 
 
@@ -55,6 +58,25 @@ def test_flash_attention(dtype, n, d, causal, cfg):
           flush=True)
     atol = {"float16": 2e-3, "float32": 1e-5, "bfloat16": 2e-2}[dtype]
     np.testing.assert_allclose(got, want, atol=atol, rtol=atol)
+
+
+@pytest.mark.parametrize("mode", ["no_split_sink", "no_split_stages", "no_acc_transpose"])
+@pytest.mark.parametrize("causal", [True, False])
+def test_flash_attention_emitter_switches(mode, causal, monkeypatch):
+    """The orders and layouts the emitter switches restore stay correct (ragged length,
+    the split-stage tile)."""
+    import torch
+    from examples.flash_attention import attention
+    print(f"[case] attention bf16 n=300 d=128 causal={causal} 128x128/4 mode={mode}", flush=True)
+    monkeypatch.setenv("ENCELADUS_CODEGEN", mode)
+    rng = np.random.default_rng(300)
+    q32, k32, v32 = (rng.standard_normal((1, 2, 300, 128)).astype(np.float32) for _ in range(3))
+    q, k, v = (torch.from_numpy(x).to(torch.bfloat16).cuda() for x in (q32, k32, v32))
+    o = attention(q, k, v, causal, 0.3, block_m=128, block_n=128, num_warps=4)
+    torch.cuda.synchronize()
+    qf, kf, vf = (x.cpu().float().numpy() for x in (q, k, v))
+    want = R.attention(qf, kf, vf, causal, 0.3)
+    np.testing.assert_allclose(o.cpu().float().numpy(), want, atol=2e-2, rtol=2e-2)
 
 
 @enceladus.jit

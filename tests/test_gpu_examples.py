@@ -241,6 +241,22 @@ def test_matmul_gemm_template(m, n, k, bm, bn, bk, nw):
     np.testing.assert_allclose(got, want, rtol=2e-3, atol=1e-3)
 
 
+@pytest.mark.parametrize("kind", ["template", "pointer"])
+def test_matmul_without_transposed_accumulator(kind, monkeypatch):
+    """ENCELADUS_CODEGEN=no_acc_transpose (the MFMA's own accumulator orientation) on the
+    template main loop and on the generic dot lowering, ragged edges included."""
+    from examples.matmul import matmul, matmul_desc
+    _say(f"matmul {kind} 320x272x200 no_acc_transpose")
+    monkeypatch.setenv("ENCELADUS_CODEGEN", "no_acc_transpose")
+    a, b = _half((320, 200), 0, 1 / 8), _half((200, 272), 1, 1 / 8)
+    if kind == "template":
+        got = matmul_desc(a, b, bm=128, bn=128, bk=64, num_warps=4)
+    else:
+        got = matmul(a, b)
+    want = R.matmul(a, b).astype(np.float32)
+    np.testing.assert_allclose(got.astype(np.float32), want, rtol=2e-3, atol=1e-3)
+
+
 def test_matmul_template_row_tails():
     """Row strides that are multiples of 16 elements around K and N that are not multiples of
     8: the last partial 16-byte chunk of each row is read, not dropped."""
