@@ -525,7 +525,7 @@ _KERNELS = {"vector_add": ["ek_add_kernel"], "softmax": ["ek_softmax_kernel"],
 
 def profile_commands(pins: str) -> list[str]:
     """The rocprofv3 passes the summaries come from, as run on the GPU box after
-    `R=<repository root>; D=$R/gpurun_out/prof; cd /tmp && export TMPDIR=/tmp`; the pins
+    `R=<repository root>; D=<output directory>; cd /tmp && export TMPDIR=/tmp`; the pins
     come from `python3 $R/bench.py --print-pins $D/trace_bench.json`."""
     return [
         "rocprofv3 --kernel-trace --stats -d $D/trace -o run --output-format csv -- "
@@ -591,7 +591,7 @@ def summarize_profiles(d: str) -> None:
         commit = "unknown"
     pins = profile_pins(tj)
     cmds = profile_commands(pins)
-    head = ["MI355X (gfx950, 256 CUs), one GPU, ROCm 7.2 rocprofv3; numbers from one gpurun box",
+    head = ["MI355X (gfx950, 256 CUs), one GPU, ROCm 7.2 rocprofv3; numbers from one GPU box",
             f"source_stamp: {stamp}",
             f"commit: {commit}",
             "(bench.py --print-stamp gives a tree's stamp; bench.py reports traffic from this "
@@ -617,10 +617,10 @@ def summarize_profiles(d: str) -> None:
             vendor[key].append(dur)
     out = ["rocprofv3 kernel trace of every bench.py workload (BASELINE configs, the copy, "
            "read and write ceilings) and the vendor libraries"] + head + [
-        "command (on the GPU box; R = repository root, D = $R/gpurun_out/prof, run in /tmp "
+        "command (on the GPU box; R = repository root, D = the output directory, run in /tmp "
         "with TMPDIR=/tmp):",
         "  " + cmds[0],
-        "tabulated with: python bench.py --summarize-profiles gpurun_out/prof", "",
+        "tabulated with: python bench.py --summarize-profiles $D", "",
         "Per workload: the bench's HIP-event time, then the per-dispatch durations from",
         "run_kernel_trace.csv grouped by (kernel, grid in workgroups, workgroup size, LDS,",
         "registers). '*' marks the dispatches of the variant the bench reports, told apart from",
@@ -691,7 +691,7 @@ def summarize_profiles(d: str) -> None:
         "commands (on the GPU box, as for the kernel trace), one counter per run, each workload",
         "pinned to the variant the trace pass's bench reported:",
         "  " + cmds[1], "  " + cmds[2],
-        "tabulated with: python bench.py --summarize-profiles gpurun_out/prof", "",
+        "tabulated with: python bench.py --summarize-profiles $D", "",
         "calibration (copy_calib: a 256 MiB torch device copy, 262144 KiB read and 262144 KiB "
         "written):",
         f"  FETCH_SIZE per dispatch: {m(fcal):.0f} KiB -> factor {ff:.3f}",
@@ -745,7 +745,7 @@ def summarize_profiles(d: str) -> None:
     out = ["rocprofv3 SQ counters of the MFMA workloads (the variants the bench reports)"] + \
         head + ["command (on the GPU box, as for the kernel trace):",
                 "  " + cmds[3],
-                "tabulated with: python bench.py --summarize-profiles gpurun_out/prof", "",
+                "tabulated with: python bench.py --summarize-profiles $D", "",
                 "Counters are summed over the chip; per SIMD = / 1024 (256 CUs x 4 SIMDs). One",
                 "v_mfma_f32_32x32x16 is 32768 FLOP and occupies its SIMD's MFMA unit for 32",
                 "cycles. No clock is derived from these counters: the counters' window is longer",
