@@ -57,17 +57,20 @@ template <> struct int_limits<uint16_t> { static constexpr float lo = 0.f, hi = 
 
 // float -> integer: truncate toward zero; NaN -> 0; out of range saturates (all widths
 // except int64, which wraps modulo 2^64 and maps infinities to 0).
+// v_cvt_i32_f32 / v_cvt_u32_f32 implement exactly that for 32 bits (the ISA: out-of-range
+// values, infinities included, saturate and NaN converts to 0), so they are issued as is:
+// one instruction instead of a NaN test and two clamps, which the compiler emits as nested
+// branches. C++'s (int)x leaves out-of-range values undefined, hence the inline asm.
 template <typename T> EK_INLINE T f2i(float x);
 template <> EK_INLINE int32_t f2i<int32_t>(float x) {
-  if (x != x) return 0;
-  if (x >= 2147483648.0f) return 2147483647;
-  if (x <= -2147483648.0f) return (int32_t)0x80000000u;
-  return (int32_t)x;
+  int32_t r;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(x));
+  return r;
 }
 template <> EK_INLINE uint32_t f2i<uint32_t>(float x) {
-  if (x != x || x <= 0.0f) return 0u;
-  if (x >= 4294967296.0f) return 0xffffffffu;
-  return (uint32_t)x;
+  uint32_t r;
+  asm("v_cvt_u32_f32 %0, %1" : "=v"(r) : "v"(x));
+  return r;
 }
 template <> EK_INLINE uint64_t f2i<uint64_t>(float x) {
   if (x != x || x <= 0.0f) return 0ull;
@@ -86,12 +89,12 @@ template <> EK_INLINE int64_t f2i<int64_t>(float x) {
   if (r < -9223372036854775808.0) r += 18446744073709551616.0;
   return (int64_t)r;
 }
-#define EK_SMALL_F2I(T)                                          \
-  template <> EK_INLINE T f2i<T>(float x) {                      \
-    if (x != x) return 0;                                        \
-    if (x <= int_limits<T>::lo) return (T)int_limits<T>::lo;     \
-    if (x >= int_limits<T>::hi) return (T)int_limits<T>::hi;     \
-    return (T)(int32_t)x;                                        \
+// 8/16-bit: the saturating 32-bit conversion, then a clamp (truncation commutes with it).
+#define EK_SMALL_F2I(T)                                                       \
+  template <> EK_INLINE T f2i<T>(float x) {                                   \
+    const int32_t i = f2i<int32_t>(x);                                        \
+    const int32_t lo = (int32_t)int_limits<T>::lo, hi = (int32_t)int_limits<T>::hi; \
+    return (T)(i < lo ? lo : (i > hi ? hi : i));                              \
   }
 EK_SMALL_F2I(int8_t)
 EK_SMALL_F2I(uint8_t)
